@@ -1,0 +1,54 @@
+/*
+ * zonos3_gdn.h -- C ABI of the MI355X (gfx950) gated-DeltaNet kernels.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream (as void*, NULL = the default
+ * stream), launches asynchronously on that stream, allocates nothing, never synchronises the host and is
+ * therefore capturable into a HIP graph. Return value: ZGDN_OK, or an error code with a message available
+ * from zgdn_last_error() (per calling thread).
+ *
+ * Layouts (all contiguous, row-major, the reference's FLA calling convention):
+ *   q, k          [B, T, Hk, K]     v, o  [B, T, Hv, V]     g (log decay), beta  [B, T, Hv]
+ *   state         [N, Hv, V, K] float32, value-major ("state_v_first"); N = B, or the number of packed
+ *                 sequences when cu_seqlens [N+1] (int32) is given with B == 1.
+ * Grouped value heads: v-head h reads k-head h / (Hv / Hk).
+ */
+#ifndef ZONOS3_GDN_H
+#define ZONOS3_GDN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of the tensors handed over. */
+enum zgdn_dtype { ZGDN_F32 = 0, ZGDN_BF16 = 1 };
+
+/* Status codes. */
+enum zgdn_status { ZGDN_OK = 0, ZGDN_EINVAL = 1, ZGDN_EHIP = 2, ZGDN_EUNSUPPORTED = 3 };
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char* zgdn_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int zgdn_abi_version(void);
+
+/*
+ * Token-by-token gated delta rule (recurrent form), T >= 1 tokens per sequence; T == 1 is the decode step.
+ * Replaces the token loop of model/src/zonos3/reference/lm.py:574-583 (S *= a; p = S.k; d = beta (v - p);
+ * S += d k^T; o = S.(q scale)), which the serving layer otherwise recomputes through a 64-row chunk window
+ * (servers/sgl/src/zonos3_sgl/models/gdn.py:329-355).
+ *   g, beta: dtype gb_dtype (F32 or BF16); g is the log decay (alpha = exp(g)).
+ *   initial_state: NULL = zeros. final_state: NULL = not written; may equal initial_state (in place).
+ *   o: dtype o_dtype. K must be 64 or 128; V >= 1; Hv % Hk == 0.
+ */
+int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                       const void* beta, int gb_dtype, const float* initial_state, float* final_state,
+                       void* o, int o_dtype, const int32_t* cu_seqlens, int n_seqs, int B, int T, int Hk,
+                       int Hv, int K, int V, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZONOS3_GDN_H */

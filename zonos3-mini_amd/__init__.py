@@ -1,0 +1,12 @@
+"""MI355X-native (gfx950) gated-DeltaNet token mixer of ZONOS3-Mini.
+
+Hand-written HIP kernels behind a C ABI (``include/zonos3_gdn.h``, ``libzonos3_gdn.so``), driven from
+PyTorch-ROCm. Public surface:
+
+* ``ops``: direct ops (``recurrent_fwd``, ``decode_step``).
+"""
+
+from . import ops  # noqa: F401
+from .ops import decode_step, recurrent_fwd  # noqa: F401
+
+__all__ = ["ops", "recurrent_fwd", "decode_step"]

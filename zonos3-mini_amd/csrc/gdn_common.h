@@ -1,0 +1,114 @@
+// Shared device helpers for the gated-DeltaNet kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "zonos3_gdn.h"
+
+namespace zgdn {
+
+// ------------------------------------------------------------------------------------------------ bf16 storage
+
+struct bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round-to-nearest-even float -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T>
+struct io;
+
+template <>
+struct io<float> {
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float x) { *p = x; }
+  // Four consecutive elements as floats.
+  __device__ __forceinline__ static float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ static void store4(float* p, float4 x) { *reinterpret_cast<float4*>(p) = x; }
+};
+
+template <>
+struct io<bf16> {
+  __device__ __forceinline__ static float load(const bf16* p) { return bf16_to_f32(p->bits); }
+  __device__ __forceinline__ static void store(bf16* p, float x) { p->bits = f32_to_bf16(x); }
+  __device__ __forceinline__ static float4 load4(const bf16* p) {
+    uint2 w = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+  }
+  __device__ __forceinline__ static void store4(bf16* p, float4 x) {
+    uint2 w;
+    w.x = (uint32_t)f32_to_bf16(x.x) | ((uint32_t)f32_to_bf16(x.y) << 16);
+    w.y = (uint32_t)f32_to_bf16(x.z) | ((uint32_t)f32_to_bf16(x.w) << 16);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+};
+
+// --------------------------------------------------------------------------------------- cross-lane reductions
+
+// DPP move of a float within a row of 16 lanes (every source lane is valid for the patterns used here).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm(1,0,3,2)
+constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm(2,3,0,1)
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <-> 7-i within each 8-lane half row
+constexpr int DPP_ROW_MIRROR = 0x140;     // lane i <-> 15-i within each 16-lane row
+
+// Sum over aligned groups of N lanes (N = 4, 8 or 16); every lane of a group receives the group sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 4 || N == 8 || N == 16, "group of 4, 8 or 16 lanes");
+  x += dpp<DPP_QUAD_XOR1>(x);
+  x += dpp<DPP_QUAD_XOR2>(x);
+  if constexpr (N >= 8) x += dpp<DPP_ROW_HALF_MIRROR>(x);
+  if constexpr (N >= 16) x += dpp<DPP_ROW_MIRROR>(x);
+  return x;
+}
+
+// Sum over all 64 lanes of a wave (result valid in every lane).
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group_sum<16>(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// -------------------------------------------------------------------------------------------------- math
+
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte accesses for data that is touched exactly once.
+__device__ __forceinline__ float4 nt_load(const float* p) {
+  f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void nt_store(float* p, float4 x) {
+  f32x4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+}  // namespace zgdn
+
+// ------------------------------------------------------------------------------------------- host-side errors
+
+namespace zgdn {
+// Records a message for zgdn_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace zgdn

@@ -1,0 +1,190 @@
+// Recurrent gated delta rule (token-by-token), including the single-token decode step.
+//
+// Layout of the work: the value-major state [N, Hv, V, K] splits into independent rows S[n, h, j, :] (one
+// value index j each). A row of K fp32 is held by LPR = K/8 lanes of a wave, 8 floats per lane, as two
+// 16-byte pieces at columns c..c+3 and K/2+c..K/2+c+3 (c = 4 * lane-in-row), so each 128-bit load or store
+// instruction of a wave covers 64/LPR rows' contiguous halves. A wave walks PASSES such row groups; the
+// state stays in registers across tokens and is read and written exactly once per call, with non-temporal
+// 128-bit accesses. Row dot products reduce over the LPR lanes with DPP.
+//
+// Per token and row (lm.py:574-583 rewritten with one read of S):
+//   pk = S.k, pq = S.q (S before decay), alpha = exp(g)
+//   delta = beta (v_j - alpha pk)
+//   S <- alpha S + delta k
+//   o_j = scale (alpha pq + delta (k.q))            (== S_new . q scale)
+#include "gdn_common.h"
+
+namespace zgdn {
+namespace {
+
+constexpr int PASSES = 4;
+constexpr int NWAVES = 4;
+
+template <typename TIn, typename TOut, typename TG, int K>
+__global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TG* __restrict__ g,
+    const TG* __restrict__ beta, const float* s_in, float* s_out, TOut* __restrict__ o,
+    const int32_t* __restrict__ cu, int T, int Hk, int Hv, int V, float scale) {
+  constexpr int LPR = K / 8;         // lanes per state row
+  constexpr int RPP = 64 / LPR;      // rows per pass of a wave
+  constexpr int ROWS_WAVE = RPP * PASSES;
+  constexpr int ROWS_WG = ROWS_WAVE * NWAVES;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane % LPR;
+  const int rsub = lane / LPR;
+  const int c0 = sub * 4;
+  const int c1 = K / 2 + sub * 4;
+
+  const int n = blockIdx.z;
+  const int h = blockIdx.y;
+  const int hk = h / (Hv / Hk);
+  int bos, eos;
+  if (cu != nullptr) {
+    bos = cu[n];
+    eos = cu[n + 1];
+  } else {
+    bos = n * T;
+    eos = bos + T;
+  }
+  const int row0 = blockIdx.x * ROWS_WG + wave * ROWS_WAVE + rsub;
+
+  float s[PASSES][8];
+  const size_t head_base = ((size_t)n * Hv + h) * (size_t)V;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = row0 + p * RPP;
+    if (s_in != nullptr && row < V) {
+      const float* src = s_in + (head_base + row) * K;
+      float4 a = nt_load(src + c0);
+      float4 b = nt_load(src + c1);
+      s[p][0] = a.x; s[p][1] = a.y; s[p][2] = a.z; s[p][3] = a.w;
+      s[p][4] = b.x; s[p][5] = b.y; s[p][6] = b.z; s[p][7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[p][i] = 0.f;
+    }
+  }
+
+  for (int t = bos; t < eos; ++t) {
+    const size_t qk_off = ((size_t)t * Hk + hk) * K;
+    float4 ka = io<TIn>::load4(k + qk_off + c0), kb = io<TIn>::load4(k + qk_off + c1);
+    float4 qa = io<TIn>::load4(q + qk_off + c0), qb = io<TIn>::load4(q + qk_off + c1);
+    const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+    const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const size_t gh = (size_t)t * Hv + h;
+    const float alpha = __expf(io<TG>::load(g + gh));
+    const float bt = io<TG>::load(beta + gh);
+    float kq = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kq = fmaf(kk[i], qq[i], kq);
+    kq = group_sum<LPR>(kq);
+    const size_t v_base = gh * (size_t)V;
+    float vj[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + p * RPP;
+      const float x = io<TIn>::load(v + v_base + min(row, V - 1));  // clamped: no divergent load
+      vj[p] = row < V ? x : 0.f;
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + p * RPP;
+      float pk = 0.f, pq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pk = fmaf(s[p][i], kk[i], pk);
+        pq = fmaf(s[p][i], qq[i], pq);
+      }
+      pk = group_sum<LPR>(pk);
+      pq = group_sum<LPR>(pq);
+      const float delta = bt * (vj[p] - alpha * pk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[p][i] = fmaf(delta, kk[i], alpha * s[p][i]);
+      if (sub == 0 && row < V) io<TOut>::store(o + v_base + row, scale * fmaf(delta, kq, alpha * pq));
+    }
+  }
+
+  if (s_out != nullptr) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + p * RPP;
+      if (row < V) {
+        float* dst = s_out + (head_base + row) * K;
+        nt_store(dst + c0, make_float4(s[p][0], s[p][1], s[p][2], s[p][3]));
+        nt_store(dst + c1, make_float4(s[p][4], s[p][5], s[p][6], s[p][7]));
+      }
+    }
+  }
+}
+
+template <typename TIn, typename TOut, typename TG, int K>
+void launch(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s_in,
+            float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V, float scale,
+            hipStream_t stream) {
+  constexpr int ROWS_WG = (64 / (K / 8)) * PASSES * NWAVES;
+  dim3 grid((V + ROWS_WG - 1) / ROWS_WG, Hv, N);
+  hipLaunchKernelGGL((recurrent_kernel<TIn, TOut, TG, K>), grid, dim3(64 * NWAVES), 0, stream,
+                     (const TIn*)q, (const TIn*)k, (const TIn*)v, (const TG*)g, (const TG*)beta, s_in, s_out,
+                     (TOut*)o, cu, T, Hk, Hv, V, scale);
+}
+
+template <typename TIn, typename TOut, typename TG>
+void launch_k(int K, const void* q, const void* k, const void* v, const void* g, const void* beta,
+              const float* s_in, float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V,
+              float scale, hipStream_t stream) {
+  if (K == 128)
+    launch<TIn, TOut, TG, 128>(q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+  else
+    launch<TIn, TOut, TG, 64>(q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+}
+
+template <typename TIn, typename TOut>
+void launch_g(int gb_dtype, int K, const void* q, const void* k, const void* v, const void* g, const void* beta,
+              const float* s_in, float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V,
+              float scale, hipStream_t stream) {
+  if (gb_dtype == ZGDN_F32)
+    launch_k<TIn, TOut, float>(K, q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+  else
+    launch_k<TIn, TOut, bf16>(K, q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+}
+
+}  // namespace
+}  // namespace zgdn
+
+extern "C" int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                                  const void* beta, int gb_dtype, const float* initial_state,
+                                  float* final_state, void* o, int o_dtype, const int32_t* cu_seqlens,
+                                  int n_seqs, int B, int T, int Hk, int Hv, int K, int V, float scale,
+                                  void* stream) {
+  using namespace zgdn;
+  const char* fn = "zgdn_recurrent_fwd";
+  if (!q || !k || !v || !g || !beta || !o) return fail(ZGDN_EINVAL, "%s: null tensor pointer", fn);
+  if (B < 1 || T < 0 || Hk < 1 || Hv < 1 || V < 1)
+    return fail(ZGDN_EINVAL, "%s: bad sizes B=%d T=%d Hk=%d Hv=%d V=%d", fn, B, T, Hk, Hv, V);
+  if (Hv % Hk) return fail(ZGDN_EINVAL, "%s: Hv=%d is not a multiple of Hk=%d", fn, Hv, Hk);
+  if (K != 64 && K != 128) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d (supported: 64, 128)", fn, K);
+  for (int dt : {qkv_dtype, gb_dtype, o_dtype})
+    if (dt != ZGDN_F32 && dt != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: unknown dtype code %d", fn, dt);
+  int N = B;
+  if (cu_seqlens != nullptr) {
+    if (B != 1) return fail(ZGDN_EINVAL, "%s: cu_seqlens needs B == 1 (got B=%d)", fn, B);
+    if (n_seqs < 1) return fail(ZGDN_EINVAL, "%s: n_seqs=%d with cu_seqlens", fn, n_seqs);
+    N = n_seqs;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (qkv_dtype == ZGDN_F32 && o_dtype == ZGDN_F32)
+    launch_g<float, float>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
+                           Hv, V, scale, s);
+  else if (qkv_dtype == ZGDN_F32)
+    launch_g<float, bf16>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
+                          Hv, V, scale, s);
+  else if (o_dtype == ZGDN_F32)
+    launch_g<bf16, float>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
+                          Hv, V, scale, s);
+  else
+    launch_g<bf16, bf16>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
+                         Hv, V, scale, s);
+  return check_launch(fn);
+}

@@ -1,0 +1,107 @@
+"""Torch-level entry points of the gated-DeltaNet kernels (validation, allocation, stream plumbing).
+
+Every function validates shapes, dtypes, devices and contiguity and raises ``RuntimeError`` on a mismatch
+(the reference layer's error style, ``servers/sgl/src/zonos3_sgl/models/gdn.py:152, 242, 255``), allocates
+outputs with torch's caching allocator, and launches on the current HIP stream of the tensors' device
+without synchronising the host, so every call can be captured into a HIP graph. There is no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from ._native import BF16, F32
+
+_CODES = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _code(t: torch.Tensor, name: str) -> int:
+    _require(t.dtype in _CODES, f"{name}: dtype {t.dtype} not supported (float32 or bfloat16)")
+    return _CODES[t.dtype]
+
+
+def _on_gpu(name: str, t: torch.Tensor, device: torch.device | None = None) -> None:
+    _require(isinstance(t, torch.Tensor), f"{name}: expected a tensor")
+    _require(t.is_cuda, f"{name}: must be a GPU tensor (got device {t.device}); there is no CPU path")
+    _require(t.is_contiguous(), f"{name}: must be contiguous")
+    if device is not None:
+        _require(t.device == device, f"{name}: on {t.device}, expected {device}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _cu_check(cu_seqlens: torch.Tensor, total: int, device) -> int:
+    _on_gpu("cu_seqlens", cu_seqlens, device)
+    _require(cu_seqlens.dtype == torch.int32, "cu_seqlens: must be int32")
+    _require(cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 2, "cu_seqlens: must be 1-D with >= 2 entries")
+    return cu_seqlens.numel() - 1
+
+
+def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
+                  final_state=None):
+    """Token-by-token gated delta rule (lm.py:574-583 in FLA's calling convention).
+
+    q, k [B, T, Hk, K]; v [B, T, Hv, V]; g (log decay) and beta [B, T, Hv], float32 or bfloat16;
+    initial_state [N, Hv, V, K] float32 or None (zeros); cu_seqlens int32 [N+1] with B == 1 for packed
+    sequences. ``final_state`` may name an existing float32 tensor to write (it may be ``initial_state``
+    itself: an in-place update). Returns (o [B, T, Hv, V] in v's dtype, final state or None)."""
+    _on_gpu("q", q)
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
+        _on_gpu(name, t, dev)
+    _require(q.dim() == 4 and k.shape == q.shape, f"q, k: expected equal [B, T, Hk, K], got {tuple(q.shape)}, "
+                                                  f"{tuple(k.shape)}")
+    B, T, Hk, K = q.shape
+    _require(v.dim() == 4 and v.shape[:2] == (B, T), f"v: expected [B={B}, T={T}, Hv, V], got {tuple(v.shape)}")
+    Hv, V = v.shape[2], v.shape[3]
+    _require(Hv % Hk == 0, f"value heads ({Hv}) must be a multiple of key heads ({Hk})")
+    _require(g.shape == (B, T, Hv) and beta.shape == (B, T, Hv), f"g, beta: expected [{B}, {T}, {Hv}]")
+    _require(q.dtype == k.dtype == v.dtype, "q, k, v: must share a dtype")
+    _require(g.dtype == beta.dtype, "g, beta: must share a dtype")
+    qkv_code, gb_code = _code(q, "q"), _code(g, "g")
+    n_seqs = B
+    if cu_seqlens is not None:
+        _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        n_seqs = _cu_check(cu_seqlens, T, dev)
+    if initial_state is not None:
+        _on_gpu("initial_state", initial_state, dev)
+        _require(initial_state.dtype == torch.float32, "initial_state: must be float32")
+        _require(initial_state.shape == (n_seqs, Hv, V, K),
+                 f"initial_state: expected [{n_seqs}, {Hv}, {V}, {K}], got {tuple(initial_state.shape)}")
+    if final_state is not None:
+        _on_gpu("final_state", final_state, dev)
+        _require(final_state.dtype == torch.float32 and final_state.shape == (n_seqs, Hv, V, K),
+                 f"final_state: expected float32 [{n_seqs}, {Hv}, {V}, {K}]")
+    elif output_final_state:
+        final_state = torch.empty(n_seqs, Hv, V, K, device=dev, dtype=torch.float32)
+    o = torch.empty(B, T, Hv, V, device=dev, dtype=v.dtype)
+    scale = K**-0.5 if scale is None else float(scale)
+    _native.call(
+        "zgdn_recurrent_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), qkv_code, g.data_ptr(), beta.data_ptr(),
+        gb_code, _ptr(initial_state), _ptr(final_state), o.data_ptr(), _code(o, "o"), _ptr(cu_seqlens), n_seqs,
+        B, T, Hk, Hv, K, V, scale, _stream(dev),
+    )
+    return o, final_state
+
+
+def decode_step(q, k, v, g, beta, state, scale=None):
+    """One single-token step for B independent streams, updating ``state`` in place.
+
+    q, k [B, Hk, K]; v [B, Hv, V]; g (log decay), beta [B, Hv]; state [B, Hv, V, K] float32.
+    Returns o [B, Hv, V] in v's dtype (the recurrence of lm.py:574-583 at T = 1)."""
+    _require(q.dim() == 3 and v.dim() == 3, "decode_step: q, k [B, Hk, K] and v [B, Hv, V] expected")
+    o, _ = recurrent_fwd(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), g.unsqueeze(1), beta.unsqueeze(1),
+                         scale=scale, initial_state=state, final_state=state)
+    return o.squeeze(1)
