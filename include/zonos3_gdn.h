@@ -15,6 +15,7 @@
 #ifndef ZONOS3_GDN_H
 #define ZONOS3_GDN_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -46,6 +47,32 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
                        const void* beta, int gb_dtype, const float* initial_state, float* final_state,
                        void* o, int o_dtype, const int32_t* cu_seqlens, int n_seqs, int B, int T, int Hk,
                        int Hv, int K, int V, float scale, void* stream);
+
+/*
+ * Bytes of workspace zgdn_chunk_fwd needs for n_chunks 64-token chunks (over all sequences) and Hv value
+ * heads (98,560 bytes per chunk and head).
+ */
+size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
+
+/*
+ * Chunked (WY/UT form, 64-token chunks) gated delta rule over whole sequences on bf16 MFMA with fp32
+ * accumulation: the prefill core. Replaces FLA's chunk_gated_delta_rule_fwd as called at
+ * servers/sgl/src/zonos3_sgl/models/gdn.py:418-434 (state_v_first=True, chunk_size=64, output o and the
+ * final state), itself the chunked form of model/src/zonos3/reference/lm.py:574-583.
+ *   q, k, v: bf16, K == V == 128. o: bf16 [B, T, Hv, V].
+ *   g, beta: gb_dtype. With A_log and dt_bias (float32 [Hv], both or neither) g holds the raw gate input a
+ *   and the log decay is -exp(A_log[h]) * softplus(a + dt_bias[h]) (FLA use_gate_in_kernel=True,
+ *   gdn.py:430-432); otherwise g is the log decay.
+ *   cu_seqlens [n_seqs+1] + chunk_indices [n_chunks, 2] (sequence, chunk within it; the table of
+ *   gdn.py:49-59) for packed sequences (B == 1); otherwise n_chunks is derived from B and T.
+ *   initial_state NULL = zeros; final_state NULL = not written; may equal initial_state (in place).
+ *   workspace: device memory of at least zgdn_chunk_workspace_size(n_chunks, Hv) bytes.
+ */
+int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g, const void* beta,
+                   int gb_dtype, const float* A_log, const float* dt_bias, const float* initial_state,
+                   float* final_state, void* o, const int32_t* cu_seqlens, const int32_t* chunk_indices,
+                   int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K, int V, float scale,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -8,7 +8,7 @@ There is no fallback: a missing or unloadable library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libzonos3_gdn.so"
@@ -29,6 +29,12 @@ SIGNATURES: dict[str, tuple] = {
         c_int,
         [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, _P, c_int,
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
+    ),
+    "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
+    "zgdn_chunk_fwd": (
+        c_int,
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
+         c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, c_size_t, _P],
     ),
 }
 

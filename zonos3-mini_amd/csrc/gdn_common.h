@@ -91,18 +91,6 @@ __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1p
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// Streaming (non-temporal) 16-byte accesses for data that is touched exactly once.
-__device__ __forceinline__ float4 nt_load(const float* p) {
-  f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ void nt_store(float* p, float4 x) {
-  f32x4 v = {x.x, x.y, x.z, x.w};
-  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
-}
-
 }  // namespace zgdn
 
 // ------------------------------------------------------------------------------------------- host-side errors

@@ -4,8 +4,9 @@
 // value index j each). A row of K fp32 is held by LPR = K/8 lanes of a wave, 8 floats per lane, as two
 // 16-byte pieces at columns c..c+3 and K/2+c..K/2+c+3 (c = 4 * lane-in-row), so each 128-bit load or store
 // instruction of a wave covers 64/LPR rows' contiguous halves. A wave walks PASSES such row groups; the
-// state stays in registers across tokens and is read and written exactly once per call, with non-temporal
-// 128-bit accesses. Row dot products reduce over the LPR lanes with DPP.
+// state stays in registers across tokens and is read and written exactly once per call with 128-bit
+// accesses (ordinary ones: on gfx950 the non-temporal forms measured slower for this stream). Row dot
+// products reduce over the LPR lanes with DPP.
 //
 // Per token and row (lm.py:574-583 rewritten with one read of S):
 //   pk = S.k, pq = S.q (S before decay), alpha = exp(g)
@@ -17,10 +18,16 @@
 namespace zgdn {
 namespace {
 
-constexpr int PASSES = 4;
-constexpr int NWAVES = 4;
+// Default tiling: PASSES row groups per wave, NWAVES waves per workgroup.
+#ifndef ZGDN_REC_PASSES
+#define ZGDN_REC_PASSES 1
+#endif
+#ifndef ZGDN_REC_NWAVES
+#define ZGDN_REC_NWAVES 8
+#endif
 
-template <typename TIn, typename TOut, typename TG, int K>
+template <typename TIn, typename TOut, typename TG, int K, int PASSES = ZGDN_REC_PASSES,
+          int NWAVES = ZGDN_REC_NWAVES>
 __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TG* __restrict__ g,
     const TG* __restrict__ beta, const float* s_in, float* s_out, TOut* __restrict__ o,
@@ -57,8 +64,8 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
     const int row = row0 + p * RPP;
     if (s_in != nullptr && row < V) {
       const float* src = s_in + (head_base + row) * K;
-      float4 a = nt_load(src + c0);
-      float4 b = nt_load(src + c1);
+      float4 a = io<float>::load4(src + c0);
+      float4 b = io<float>::load4(src + c1);
       s[p][0] = a.x; s[p][1] = a.y; s[p][2] = a.z; s[p][3] = a.w;
       s[p][4] = b.x; s[p][5] = b.y; s[p][6] = b.z; s[p][7] = b.w;
     } else {
@@ -112,8 +119,8 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
       const int row = row0 + p * RPP;
       if (row < V) {
         float* dst = s_out + (head_base + row) * K;
-        nt_store(dst + c0, make_float4(s[p][0], s[p][1], s[p][2], s[p][3]));
-        nt_store(dst + c1, make_float4(s[p][4], s[p][5], s[p][6], s[p][7]));
+        io<float>::store4(dst + c0, make_float4(s[p][0], s[p][1], s[p][2], s[p][3]));
+        io<float>::store4(dst + c1, make_float4(s[p][4], s[p][5], s[p][6], s[p][7]));
       }
     }
   }
@@ -123,6 +130,7 @@ template <typename TIn, typename TOut, typename TG, int K>
 void launch(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s_in,
             float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V, float scale,
             hipStream_t stream) {
+  constexpr int PASSES = ZGDN_REC_PASSES, NWAVES = ZGDN_REC_NWAVES;
   constexpr int ROWS_WG = (64 / (K / 8)) * PASSES * NWAVES;
   dim3 grid((V + ROWS_WG - 1) / ROWS_WG, Hv, N);
   hipLaunchKernelGGL((recurrent_kernel<TIn, TOut, TG, K>), grid, dim3(64 * NWAVES), 0, stream,

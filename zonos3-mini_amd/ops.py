@@ -105,3 +105,83 @@ def decode_step(q, k, v, g, beta, state, scale=None):
     o, _ = recurrent_fwd(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), g.unsqueeze(1), beta.unsqueeze(1),
                          scale=scale, initial_state=state, final_state=state)
     return o.squeeze(1)
+
+
+CHUNK = 64  # chunk length of the chunked kernels (servers/sgl/src/zonos3_sgl/models/gdn.py:46)
+
+
+def chunk_indices_from_cu(cu_seqlens: torch.Tensor) -> torch.Tensor:
+    """(sequence, chunk within it) int32 [n_chunks, 2] of packed sequences (gdn.py:49-59). Reads
+    ``cu_seqlens`` on the host (one device->host copy); callers that already hold the lengths on the host
+    build the table there, as the reference does."""
+    cu = cu_seqlens.tolist()
+    rows = [(i, j) for i in range(len(cu) - 1) for j in range(-(-(cu[i + 1] - cu[i]) // CHUNK))]
+    t = torch.tensor(rows, dtype=torch.int32).reshape(-1, 2)
+    return t.to(cu_seqlens.device)
+
+
+def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
+              chunk_indices=None, A_log=None, dt_bias=None, final_state=None):
+    """Chunked gated delta rule (64-token chunks, bf16 MFMA, fp32 state): the prefill core.
+
+    The operator behind FLA's ``chunk_gated_delta_rule_fwd`` as the serving layer calls it
+    (``servers/sgl/src/zonos3_sgl/models/gdn.py:418-434``): q, k [B, T, Hk, 128], v [B, T, Hv, 128] bf16;
+    g, beta [B, T, Hv] float32 or bfloat16. With ``A_log``/``dt_bias`` (float32 [Hv]) g is the raw gate input
+    and the decay is formed in the kernel (``use_gate_in_kernel=True``). Packed sequences: B == 1,
+    ``cu_seqlens`` int32 [N+1] and optionally ``chunk_indices`` int32 [n_chunks, 2]. Returns
+    (o [B, T, Hv, 128] bf16, final state [N, Hv, 128, 128] float32 or None)."""
+    _on_gpu("q", q)
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
+        _on_gpu(name, t, dev)
+    _require(q.dim() == 4 and k.shape == q.shape, f"q, k: expected equal [B, T, Hk, K], got {tuple(q.shape)}, "
+                                                  f"{tuple(k.shape)}")
+    B, T, Hk, K = q.shape
+    _require(v.dim() == 4 and v.shape[:2] == (B, T), f"v: expected [B={B}, T={T}, Hv, V], got {tuple(v.shape)}")
+    Hv, V = v.shape[2], v.shape[3]
+    _require(K == 128 and V == 128, f"chunk_fwd: head dims K={K}, V={V}; the chunked kernel needs 128")
+    _require(Hv % Hk == 0, f"value heads ({Hv}) must be a multiple of key heads ({Hk})")
+    _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "chunk_fwd: q, k, v must be bfloat16")
+    _require(g.shape == (B, T, Hv) and beta.shape == (B, T, Hv), f"g, beta: expected [{B}, {T}, {Hv}]")
+    _require(g.dtype == beta.dtype, "g, beta: must share a dtype")
+    gb_code = _code(g, "g")
+    if (A_log is None) != (dt_bias is None):
+        raise RuntimeError("A_log and dt_bias go together")
+    if A_log is not None:
+        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+            _on_gpu(name, t, dev)
+            _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
+    n_seqs = B
+    n_chunks = B * (-(-T // CHUNK))
+    if cu_seqlens is not None:
+        _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        n_seqs = _cu_check(cu_seqlens, T, dev)
+        if chunk_indices is None:
+            chunk_indices = chunk_indices_from_cu(cu_seqlens)
+        _on_gpu("chunk_indices", chunk_indices, dev)
+        _require(chunk_indices.dtype == torch.int32 and chunk_indices.dim() == 2 and chunk_indices.shape[1] == 2,
+                 "chunk_indices: expected int32 [n_chunks, 2]")
+        n_chunks = chunk_indices.shape[0]
+    elif chunk_indices is not None:
+        raise RuntimeError("chunk_indices without cu_seqlens")
+    if initial_state is not None:
+        _on_gpu("initial_state", initial_state, dev)
+        _require(initial_state.dtype == torch.float32 and initial_state.shape == (n_seqs, Hv, V, K),
+                 f"initial_state: expected float32 [{n_seqs}, {Hv}, {V}, {K}], got {tuple(initial_state.shape)}")
+    if final_state is not None:
+        _on_gpu("final_state", final_state, dev)
+        _require(final_state.dtype == torch.float32 and final_state.shape == (n_seqs, Hv, V, K),
+                 f"final_state: expected float32 [{n_seqs}, {Hv}, {V}, {K}]")
+    elif output_final_state:
+        final_state = torch.empty(n_seqs, Hv, V, K, device=dev, dtype=torch.float32)
+    o = torch.empty(B, T, Hv, V, device=dev, dtype=torch.bfloat16)
+    ws_bytes = int(_native.lib().zgdn_chunk_workspace_size(n_chunks, Hv))
+    workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    scale = K**-0.5 if scale is None else float(scale)
+    _native.call(
+        "zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), BF16, g.data_ptr(), beta.data_ptr(), gb_code,
+        _ptr(A_log), _ptr(dt_bias), _ptr(initial_state), _ptr(final_state), o.data_ptr(), _ptr(cu_seqlens),
+        _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, scale, workspace.data_ptr(), ws_bytes,
+        _stream(dev),
+    )
+    return o, final_state
