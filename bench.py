@@ -11,6 +11,10 @@ the whole batch; 8 consecutive steps are captured in one HIP graph and replayed.
 bf16 q, k, v, o, fp32 g and beta; x 1024 token-heads = 135,274,496 B) / its mean duration, measured with
 HIP events on the launch stream, against the 8 TB/s HBM peak.
 
+``prefill``: the chunked prefill workload (B=1, T=4096, H=16, dk=dv=128, 64-token chunks, bf16) with its
+MFMA roofline: 2 C^2 (3 dk + 2 dv) + 6 C dk dv + C^3/3 flops per chunk and head (11.90 GFLOP in all) / the
+mean duration of the path's kernels, against the 2.5 PFLOP/s dense bf16 peak.
+
 ``cpu_baseline``: the CPU oracle (a restatement of the reference's torch token loop) on the host cores, on
 the same decode step (median of 5 runs after one warm-up).
 """
@@ -59,19 +63,21 @@ STEPS_PER_GRAPH = 8
 
 
 def kernel_ms(torch, stream, fn, n):
-    """Mean duration (ms) of ``n`` back-to-back launches of ``fn``, each bracketed by HIP events on the
-    launch stream. A sleep kernel queued first keeps the GPU busy while the host enqueues every
-    (event, launch, event) triple, so no host-side gap lands inside a bracket."""
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    """Mean duration (ms) of one call of ``fn`` (its kernels), from HIP events on the launch stream around
+    ``n`` back-to-back calls. A sleep kernel queued first keeps the GPU busy while the host enqueues the
+    calls, so host launch overhead does not land between them."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(100_000_000)
-        for i in range(n):
-            starts[i].record(stream)
+        fn()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        start.record(stream)
+        for _ in range(n):
             fn()
-            ends[i].record(stream)
+        end.record(stream)
     torch.cuda.synchronize()
-    return statistics.mean(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return start.elapsed_time(end) / n
 
 
 def bench_decode(torch, gdn, steps, warmup):
@@ -100,7 +106,7 @@ def bench_decode(torch, gdn, steps, warmup):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     done = replays * STEPS_PER_GRAPH
-    k_ms = kernel_ms(torch, stream, step, 100)
+    k_ms = kernel_ms(torch, stream, step, 200)
     bytes_per_launch = DECODE_BYTES_PER_TOKEN_HEAD * DECODE["B"] * DECODE["H"]
     return {
         "steps": done,
@@ -109,6 +115,43 @@ def bench_decode(torch, gdn, steps, warmup):
         "kernel_ms": k_ms,
         "bytes_per_launch": bytes_per_launch,
         "achieved_gbs": bytes_per_launch / (k_ms * 1e-3) / 1e9,
+    }
+
+
+PREFILL = dict(B=1, T=4096, H=16, K=128, V=128, C=64)
+# flops per chunk and head: 2 C^2 (3 dk + 2 dv) + 6 C dk dv + C^3 / 3 (the WY form's matrix products)
+_C, _K, _V = PREFILL["C"], PREFILL["K"], PREFILL["V"]
+PREFILL_FLOP_PER_CHUNK_HEAD = 2 * _C * _C * (3 * _K + 2 * _V) + 6 * _C * _K * _V + _C**3 / 3
+
+
+def bench_prefill(torch, gdn, reps=50):
+    from oracle import gdn_oracle as O
+
+    dev = torch.device("cuda:0")
+    c = PREFILL
+    d = O.make_inputs(c["B"], c["T"], c["H"], c["H"], c["K"], c["V"], seed=1003, dtype=torch.bfloat16)
+    x = {n: d[n].to(dev) for n in ("q", "k", "v", "g", "beta")}
+    stream = torch.cuda.Stream(dev)
+
+    def run():
+        return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
+
+    ms = kernel_ms(torch, stream, run, reps)
+    flops = PREFILL_FLOP_PER_CHUNK_HEAD * (c["T"] // c["C"]) * c["H"] * c["B"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "workload": "chunked prefill: B=1, T=4096, H=16, dk=dv=128, chunk 64, bf16 q/k/v/o, fp32 state, "
+                    "zero initial state (both kernels of the chunked path)",
+        "tokens_per_s": round(c["B"] * c["T"] / (ms * 1e-3), 1),
+        "ms": round(ms, 5),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": int(flops),
+        },
     }
 
 
@@ -176,6 +219,7 @@ def main():
             "algorithmic_bytes": dec["bytes_per_launch"],
         },
     }
+    line["prefill"] = bench_prefill(torch, gdn)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
     print(json.dumps(line), flush=True)

@@ -1,21 +1,21 @@
 // Chunked (WY / UT form) gated delta rule prefill on bf16 MFMA, 64-token chunks, dk = dv = 128.
 //
 // Per chunk of L <= 64 tokens and value head h, with in-chunk cumulative log decay G (G_i = g_1+..+g_i), start
-// state S0 [V, K] (value-major) and scale s (derivation: the chunked statement of the oracle):
+// state S0 [V, K] (value-major) and scale s (the chunked statement of the recurrence):
 //   A  = strictly-lower( beta_i exp(G_i - G_j) k_i.k_j )           T = (I + A)^-1   (unit lower triangular)
 //   W  = T diag(beta exp(G)) K                                      [L x K]
 //   Ub = diag(beta) V + (T - I) diag(beta) V                        [L x V]   (diagonal exact in fp32)
 //   P  = s * lower-incl( exp(G_i - G_j) q_i.k_j )                   [L x L]
-//   Qp = s diag(exp(G)) Q - P W,    Ol = P Ub
-//   U  = Ub - W S0^T                (the corrected values)
-//   O  = Ol + Qp S0^T
+//   U  = Ub - W S0^T                                                (the corrected values)
+//   O  = s diag(exp(G)) Q S0^T + P U
 //   S  = exp(G_L) S0 + (diag(exp(G_L - G)) U)^T K
-// Phase 1 (chunk_prep_kernel, one workgroup per chunk x head, all independent) forms Qp, W, Ub, Ol and K^T
+// Phase 1 (chunk_prep_kernel, one workgroup per chunk x head, all independent) forms W, Ub, P, K^T and G
 // into a workspace. Phase 2 (chunk_state_kernel, one workgroup per sequence x head x 16 value rows) walks the
-// chunks in order keeping its 16 x 128 slice of the fp32 state in registers: U = Ub - W S^T and O = Ol + Qp S^T
-// are one MFMA pass over [Qp; W], the state update is a second. Numerics: MFMA operands are bf16 with fp32
-// accumulation; the decayed U enters the state update as a hi + lo bf16 pair (two MFMAs), and the diagonal
-// of T diag(beta) is applied in fp32, which keeps the fp32 state within ~1e-4 of the exact recurrence.
+// chunks in order keeping its 16 x 128 slice of the fp32 state in registers: one MFMA pass over [W; Q] gives
+// W S^T and Q S^T, then the state update and the outputs' P U are a second. The next chunk's operands are
+// prefetched into registers while the current one is processed. Numerics: MFMA operands are bf16 with fp32
+// accumulation; the decayed U enters the state update as a hi + lo bf16 pair (two MFMAs) and the diagonal of
+// T diag(beta) is applied in fp32, which keeps the fp32 state within ~1e-4 of the exact recurrence.
 //
 // MFMA used: v_mfma_f32_16x16x32_bf16 (A: row lane%16, k 8*(lane/16)+0..7; B: column lane%16, same k;
 // D: row 4*(lane/16)+i, column lane%16) and v_mfma_f32_16x16x4_f32 (A[lane%16][lane/16], B[lane/16][lane%16])
@@ -37,13 +37,12 @@ constexpr int LDC = CH + 8;  // padded LDS row (bf16) of a 64-wide matrix
 constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
 
 // Workspace of one chunk x head (bytes).
-constexpr size_t WS_QP = 0;                                 // Qp [64][128] bf16
-constexpr size_t WS_W = WS_QP + CH * DK * 2;                // W  [64][128] bf16
-constexpr size_t WS_KT = WS_W + CH * DK * 2;                // K^T [128][64] bf16
-constexpr size_t WS_UT = WS_KT + DK * CH * 2;               // Ub^T [128][64] fp32
-constexpr size_t WS_OT = WS_UT + DV * CH * 4;               // Ol^T [128][64] bf16
-constexpr size_t WS_G = WS_OT + DV * CH * 2;                // G [64] fp32
-constexpr size_t WS_CHUNK = WS_G + CH * 4;                  // 98,560 bytes
+constexpr size_t WS_W = 0;                        // W    [64][128] bf16
+constexpr size_t WS_KT = WS_W + CH * DK * 2;      // K^T  [128][64] bf16
+constexpr size_t WS_UT = WS_KT + DK * CH * 2;     // Ub^T [128][64] fp32
+constexpr size_t WS_P = WS_UT + DV * CH * 4;      // P    [64][64]  bf16
+constexpr size_t WS_G = WS_P + CH * CH * 2;       // G    [64]      fp32
+constexpr size_t WS_CHUNK = WS_G + CH * 4;        // 73,984 bytes
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
@@ -77,24 +76,6 @@ __device__ __forceinline__ f32x4 mm16_f32(const float* A, int lda, const float* 
   return acc;
 }
 
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float* out);
-template <>
-__device__ __forceinline__ void load8<bf16>(const bf16* p, float* out) {
-  uint4 w = *reinterpret_cast<const uint4*>(p);
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = __uint_as_float(u[i] << 16);
-    out[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-  }
-}
-template <>
-__device__ __forceinline__ void load8<float>(const float* p, float* out) {
-  float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w; out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-}
-
 // Token range of chunk `c`: packed sequences (cu != nullptr, chunk index table (seq, j)) or B x T batches.
 struct ChunkRange {
   int t0, len;
@@ -123,37 +104,58 @@ __device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, cons
 
 // ----------------------------------------------------------------------------------------------- phase 1
 
-constexpr int P1_WAVES = 8;
+constexpr int P1_WAVES = 4;
 
 struct Prep {
-  uint16_t KsT[DK][LDC];      // K^T   (B operand of W = TB K)
-  uint16_t VsT[DV][LDC];      // V^T   (B operand of Ub = LB V)
+  uint16_t KsT[DK][LDC];  // K^T (B operand of W = TB K)
+  uint16_t VsT[DV][LDC];  // V^T (B operand of Ub = LB V, and the exact diagonal term)
   union {
     struct {
-      uint16_t Qs[CH][LDQ];   // Q, K rows (A/B operands of K K^T, Q K^T)
+      uint16_t Qs[CH][LDQ];  // Q, K rows (operands of K K^T, Q K^T)
       uint16_t Ks[CH][LDQ];
     } a;
     struct {
-      uint16_t WsT[DK][LDC];  // W^T, Ub^T (B operands of P W, P Ub)
-      uint16_t UsT[DV][LDC];
-    } d;
+      float As[CH][LDF];  // strictly lower A (fp32)
+      float Ts[CH][LDF];  // T = (I + A)^-1 (fp32)
+    } b;
+    struct {
+      uint16_t TBs[CH][LDC];  // T diag(beta exp G)  (bf16)
+      uint16_t LBs[CH][LDC];  // (T - I) diag(beta)  (bf16)
+    } c;
   } u;
-  float As[CH][LDF];          // strictly lower A (fp32)
-  float Ts[CH][LDF];          // T = (I + A)^-1 (fp32)
-  float Ys[P1_WAVES][16][20];  // per-wave 16x16 fp32 scratch of the block inverse
-  uint16_t Ps[CH][LDC];       // P (bf16), A operand of P W and P Ub
-  uint16_t TBs[CH][LDC];      // T diag(beta exp G)
-  uint16_t LBs[CH][LDC];      // (T - I) diag(beta)
+  float Ys[P1_WAVES][16][20];  // per-wave 16x16 scratch of the block inverse
   float Gs[CH];
   float Bs[CH];
 };
 
-template <typename TIn, typename TG, bool GATE>
+// Row-pair transposed store: dst[(c8 + i) * ld + r] <- (a[i], b[i]) as one 32-bit word (rows r, r + 1).
+__device__ __forceinline__ void store_pair_t(uint16_t* dst, int ld, int c8, int r, uint4 a, uint4 b) {
+  const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    *reinterpret_cast<uint32_t*>(dst + (c8 + 2 * i) * ld + r) = (wa[i] & 0xffffu) | (wb[i] << 16);
+    *reinterpret_cast<uint32_t*>(dst + (c8 + 2 * i + 1) * ld + r) = (wa[i] >> 16) | (wb[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lower-triangle tile t (0..9) of a 4x4 block grid -> (row block, column block), row-major order.
+__device__ __forceinline__ void lower_tile(int t, int& rb, int& cb) {
+  rb = t < 1 ? 0 : (t < 3 ? 1 : (t < 6 ? 2 : 3));
+  cb = t - rb * (rb + 1) / 2;
+}
+
+template <typename TG, bool GATE>
 __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
-    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TG* __restrict__ g,
-    const TG* __restrict__ beta, const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx, int n_seqs, int T, int Hk, int Hv,
-    float scale, uint8_t* __restrict__ ws) {
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
+    int n_seqs, int T, int Hk, int Hv, float scale, uint8_t* __restrict__ ws) {
   __shared__ Prep sm;
   const int c = blockIdx.x, h = blockIdx.y;
   const int hk = h / (Hv / Hk);
@@ -161,27 +163,30 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
   const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
   uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
 
-  // 1. q, k, v rows -> LDS (zero rows past the chunk end); K^T and V^T transposed copies.
-  for (int e = tid; e < CH * (DK / 8); e += 64 * P1_WAVES) {
-    const int r = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
-    float qf[8], kf[8], vf[8];
-    if (r < cr.len) {
-      const size_t t = (size_t)(cr.t0 + r);
-      load8<TIn>(q + (t * Hk + hk) * DK + c8, qf);
-      load8<TIn>(k + (t * Hk + hk) * DK + c8, kf);
-      load8<TIn>(v + (t * Hv + h) * DV + c8, vf);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[i] = kf[i] = vf[i] = 0.f;
+  // 1. rows of q, k, v -> LDS as row pairs (zeros past the chunk end): Q, K row-major, K^T and V^T.
+  for (int item = tid; item < (CH / 2) * (DK / 8); item += 64 * P1_WAVES) {
+    const int p = item % (CH / 2), c8 = (item / (CH / 2)) * 8;
+    const int r0 = 2 * p, r1 = 2 * p + 1;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
+    if (r0 < cr.len) {
+      const size_t t = (size_t)(cr.t0 + r0);
+      q0 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
+      k0 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
+      v0 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t qb = f32_to_bf16(qf[i]), kb = f32_to_bf16(kf[i]), vb = f32_to_bf16(vf[i]);
-      sm.u.a.Qs[r][c8 + i] = qb;
-      sm.u.a.Ks[r][c8 + i] = kb;
-      sm.KsT[c8 + i][r] = kb;
-      sm.VsT[c8 + i][r] = vb;
+    if (r1 < cr.len) {
+      const size_t t = (size_t)(cr.t0 + r1);
+      q1 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
+      k1 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
+      v1 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
     }
+    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r0][c8]) = q0;
+    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r1][c8]) = q1;
+    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r0][c8]) = k0;
+    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r1][c8]) = k1;
+    store_pair_t(&sm.KsT[0][0], LDC, c8, r0, k0, k1);
+    store_pair_t(&sm.VsT[0][0], LDC, c8, r0, v0, v1);
   }
   if (wave == 0) {
     float gi = 0.f, bi = 0.f;
@@ -191,9 +196,8 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       if constexpr (GATE) gi = -__expf(A_log[h]) * softplus(gi + dt_bias[h]);
       bi = io<TG>::load(beta + gh);
     }
-    // inclusive prefix sum over the 64 lanes
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
+    for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
       const float o = __shfl_up(gi, d);
       if (l >= d) gi += o;
     }
@@ -203,94 +207,105 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // 2. K K^T and Q K^T on the lower block triangle (10 tiles each): A and P.
-  f32x4 acc[3];
-  int jobs[3];
-  int njob = 0;
-  for (int job = wave; job < 20; job += P1_WAVES) {
-    const int which = job / 10, t = job % 10;  // t -> (rb, cb) with rb >= cb
-    int rb = 0;
-    while ((rb + 1) * (rb + 2) / 2 <= t) ++rb;
-    const int cb = t - rb * (rb + 1) / 2;
-    const uint16_t* Am = which ? &sm.u.a.Qs[0][0] : &sm.u.a.Ks[0][0];
-    acc[njob] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
-    jobs[njob++] = job;
-  }
-  __syncthreads();  // every wave is done reading Qs / Ks (As, Ps do not alias them, WsT/UsT do later)
-  for (int n = 0; n < njob; ++n) {
-    const int which = jobs[n] / 10, t = jobs[n] % 10;
-    int rb = 0;
-    while ((rb + 1) * (rb + 2) / 2 <= t) ++rb;
-    const int cb = t - rb * (rb + 1) / 2;
-    const int j = cb * 16 + (l & 15);
-    const float gj = sm.Gs[j];
+  // 2. K K^T and Q K^T on the 10 lower tiles each (5 tile jobs per wave), kept in registers.
+  f32x4 acc[5];
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int i = rb * 16 + 4 * (l >> 4) + i4;
-      const float gi = sm.Gs[i];
-      if (which == 0) {
-        sm.As[i][j] = i > j ? sm.Bs[i] * __expf(gi - gj) * acc[n][i4] : 0.f;
-      } else {
-        sm.Ps[i][j] = f32_to_bf16(i >= j ? scale * __expf(gi - gj) * acc[n][i4] : 0.f);
+  for (int m = 0; m < 5; ++m) {
+    const int job = wave + P1_WAVES * m;
+    int rb, cb;
+    lower_tile(job % 10, rb, cb);
+    const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
+    acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
+  }
+  __syncthreads();  // As / Ts overwrite Qs / Ks
+  {
+    uint16_t* gP = reinterpret_cast<uint16_t*>(wsc + WS_P);
+#pragma unroll
+    for (int m = 0; m < 5; ++m) {
+      const int job = wave + P1_WAVES * m;
+      int rb, cb;
+      lower_tile(job % 10, rb, cb);
+      const int j = cb * 16 + (l & 15);
+      const float gj = sm.Gs[j];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int i = rb * 16 + 4 * (l >> 4) + i4;
+        const float e = __expf(sm.Gs[i] - gj);
+        if (job < 10) {
+          sm.u.b.As[i][j] = i > j ? sm.Bs[i] * e * acc[m][i4] : 0.f;
+        } else {
+          gP[i * CH + j] = f32_to_bf16(i >= j ? scale * e * acc[m][i4] : 0.f);
+        }
       }
     }
-  }
-  // zero the strictly upper blocks of P (6 tiles of 16x16)
-  for (int e = tid; e < 6 * 256; e += 64 * P1_WAVES) {
-    const int t = e / 256, w = e % 256;
-    const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
-    const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    sm.Ps[rb * 16 + w / 16][cb * 16 + w % 16] = 0;
+    for (int e = tid; e < 6 * 256; e += 64 * P1_WAVES) {  // zero upper blocks of P
+      const int t = e / 256, w = e % 256;
+      const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
+      const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+      gP[(rb * 16 + w / 16) * CH + cb * 16 + w % 16] = 0;
+    }
   }
   __syncthreads();
 
-  // 3a. diagonal 16x16 blocks of T by forward substitution: lane = 16 * block + column.
+  // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
   if (wave == 0) {
     const int b = l >> 4, col = l & 15, base = b * 16;
     float t[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
+      const float4* arow = reinterpret_cast<const float4*>(&sm.u.b.As[base + r][base]);
+      float a[16];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 x = arow[q4];
+        a[4 * q4] = x.x; a[4 * q4 + 1] = x.y; a[4 * q4 + 2] = x.z; a[4 * q4 + 3] = x.w;
+      }
       float s = (r == col) ? 1.f : 0.f;
 #pragma unroll
-      for (int jj = 0; jj < r; ++jj) s = fmaf(-sm.As[base + r][base + jj], t[jj], s);
+      for (int jj = 0; jj < r; ++jj) s = fmaf(-a[jj], t[jj], s);
       t[r] = s;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sm.Ts[base + r][base + col] = t[r];
-  }
-  // zero the strictly upper blocks of T
-  for (int e = tid; e < 6 * 256; e += 64 * P1_WAVES) {
-    const int t = e / 256, w = e % 256;
-    const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
-    const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    sm.Ts[rb * 16 + w / 16][cb * 16 + w % 16] = 0.f;
+    for (int r = 0; r < 16; ++r) sm.u.b.Ts[base + r][base + col] = t[r];
   }
   __syncthreads();
 
-  // 3b. off-diagonal blocks, one block row at a time: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj.
+  // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA).
   for (int bi = 1; bi < 4; ++bi) {
-    const int bj = wave;  // wave w computes block (bi, w) for w < bi
+    const int bj = wave;
     if (bj < bi) {
       f32x4 y = zero4();
-      for (int m = bj; m < bi; ++m) y = mm16_f32(&sm.As[bi * 16][m * 16], LDF, &sm.Ts[m * 16][bj * 16], LDF, y);
+      for (int m = bj; m < bi; ++m)
+        y = mm16_f32(&sm.u.b.As[bi * 16][m * 16], LDF, &sm.u.b.Ts[m * 16][bj * 16], LDF, y);
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) sm.Ys[wave][4 * (l >> 4) + i4][l & 15] = y[i4];
-    }
-    __syncthreads();
-    if (bj < bi) {
-      f32x4 z = mm16_f32(&sm.Ts[bi * 16][bi * 16], LDF, &sm.Ys[wave][0][0], 20, zero4());
+      wave_sync_lds();
+      f32x4 z = mm16_f32(&sm.u.b.Ts[bi * 16][bi * 16], LDF, &sm.Ys[wave][0][0], 20, zero4());
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sm.Ts[bi * 16 + 4 * (l >> 4) + i4][bj * 16 + (l & 15)] = -z[i4];
+      for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[bi * 16 + 4 * (l >> 4) + i4][bj * 16 + (l & 15)] = -z[i4];
     }
     __syncthreads();
   }
 
-  // 3c. TB = T diag(beta exp G), LB = (T - I) diag(beta), both bf16.
-  for (int e = tid; e < CH * CH; e += 64 * P1_WAVES) {
+  // 3c. TB = T diag(beta exp G) and LB = (T - I) diag(beta) in bf16 (through registers: they overwrite A, T).
+  uint32_t tb[CH * CH / (64 * P1_WAVES) / 2], lb[CH * CH / (64 * P1_WAVES) / 2];
+#pragma unroll
+  for (int m = 0; m < CH * CH / (64 * P1_WAVES) / 2; ++m) {
+    const int e = 2 * (tid + 64 * P1_WAVES * m);  // two adjacent columns
     const int i = e / CH, j = e % CH;
-    const float t = sm.Ts[i][j];
-    sm.TBs[i][j] = f32_to_bf16(t * sm.Bs[j] * __expf(sm.Gs[j]));
-    sm.LBs[i][j] = f32_to_bf16(i > j ? t * sm.Bs[j] : 0.f);
+    const float t0 = i >= j ? sm.u.b.Ts[i][j] : 0.f, t1 = i >= j + 1 ? sm.u.b.Ts[i][j + 1] : 0.f;
+    const float b0 = sm.Bs[j], b1 = sm.Bs[j + 1];
+    tb[m] = (uint32_t)f32_to_bf16(t0 * b0 * __expf(sm.Gs[j])) |
+            ((uint32_t)f32_to_bf16(t1 * b1 * __expf(sm.Gs[j + 1])) << 16);
+    lb[m] = (uint32_t)f32_to_bf16(i > j ? t0 * b0 : 0.f) | ((uint32_t)f32_to_bf16(i > j + 1 ? t1 * b1 : 0.f) << 16);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < CH * CH / (64 * P1_WAVES) / 2; ++m) {
+    const int e = 2 * (tid + 64 * P1_WAVES * m);
+    const int i = e / CH, j = e % CH;
+    *reinterpret_cast<uint32_t*>(&sm.u.c.TBs[i][j]) = tb[m];
+    *reinterpret_cast<uint32_t*>(&sm.u.c.LBs[i][j]) = lb[m];
   }
   __syncthreads();
 
@@ -301,28 +316,21 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     for (int job = wave; job < 64; job += P1_WAVES) {
       const int which = job >> 5, t = job & 31;
       const int rb = t >> 3, nb = t & 7;
-      const int kend = rb < 2 ? 32 : 64;  // T and LB vanish above the block diagonal
+      const int kend = rb < 2 ? 32 : 64;  // TB and LB vanish above the block diagonal
       const int n = nb * 16 + (l & 15);
       const int i0 = rb * 16 + 4 * (l >> 4);
       if (which == 0) {
-        f32x4 w = tile_mm(&sm.TBs[0][0], LDC, rb * 16, &sm.KsT[0][0], LDC, nb * 16, kend, zero4());
+        const f32x4 w = tile_mm(&sm.u.c.TBs[0][0], LDC, rb * 16, &sm.KsT[0][0], LDC, nb * 16, kend, zero4());
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const uint16_t wb = f32_to_bf16(w[i4]);
-          gW[(i0 + i4) * DK + n] = wb;
-          sm.u.d.WsT[n][i0 + i4] = wb;
-        }
+        for (int i4 = 0; i4 < 4; ++i4) gW[(i0 + i4) * DK + n] = f32_to_bf16(w[i4]);
       } else {
-        f32x4 u = tile_mm(&sm.LBs[0][0], LDC, rb * 16, &sm.VsT[0][0], LDC, nb * 16, kend, zero4());
+        const f32x4 u = tile_mm(&sm.u.c.LBs[0][0], LDC, rb * 16, &sm.VsT[0][0], LDC, nb * 16, kend, zero4());
+        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
         float4 o;
-        float* op = &o.x;
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int i = i0 + i4;
-          const float val = fmaf(sm.Bs[i], bf16_to_f32(sm.VsT[n][i]), u[i4]);
-          op[i4] = val;
-          sm.u.d.UsT[n][i] = f32_to_bf16(val);
-        }
+        o.x = fmaf(sm.Bs[i0], __uint_as_float(vv.x << 16), u[0]);
+        o.y = fmaf(sm.Bs[i0 + 1], __uint_as_float(vv.x & 0xffff0000u), u[1]);
+        o.z = fmaf(sm.Bs[i0 + 2], __uint_as_float(vv.y << 16), u[2]);
+        o.w = fmaf(sm.Bs[i0 + 3], __uint_as_float(vv.y & 0xffff0000u), u[3]);
         *reinterpret_cast<float4*>(gUT + n * CH + i0) = o;
       }
     }
@@ -332,49 +340,156 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[n][t8]);
     }
   }
-  __syncthreads();
-
-  // 5. Qp = s exp(G) Q - P W, Ol = P Ub (32 tiles each).
-  {
-    uint16_t* gQp = reinterpret_cast<uint16_t*>(wsc + WS_QP);
-    uint16_t* gOT = reinterpret_cast<uint16_t*>(wsc + WS_OT);
-    for (int job = wave; job < 64; job += P1_WAVES) {
-      const int which = job >> 5, t = job & 31;
-      const int rb = t >> 3, nb = t & 7;
-      const int kend = rb < 2 ? 32 : 64;
-      const int n = nb * 16 + (l & 15);
-      const int i0 = rb * 16 + 4 * (l >> 4);
-      if (which == 0) {
-        f32x4 pw = tile_mm(&sm.Ps[0][0], LDC, rb * 16, &sm.u.d.WsT[0][0], LDC, nb * 16, kend, zero4());
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int i = i0 + i4;
-          float qv = 0.f;
-          if (i < cr.len) qv = io<TIn>::load(q + ((size_t)(cr.t0 + i) * Hk + hk) * DK + n);
-          gQp[i * DK + n] = f32_to_bf16(scale * __expf(sm.Gs[i]) * qv - pw[i4]);
-        }
-      } else {
-        f32x4 ol = tile_mm(&sm.Ps[0][0], LDC, rb * 16, &sm.u.d.UsT[0][0], LDC, nb * 16, kend, zero4());
-        uint2 w;
-        w.x = (uint32_t)f32_to_bf16(ol[0]) | ((uint32_t)f32_to_bf16(ol[1]) << 16);
-        w.y = (uint32_t)f32_to_bf16(ol[2]) | ((uint32_t)f32_to_bf16(ol[3]) << 16);
-        *reinterpret_cast<uint2*>(gOT + n * CH + i0) = w;
-      }
-    }
-  }
 }
 
 // ----------------------------------------------------------------------------------------------- phase 2
 
-constexpr int P2_WAVES = 4;
+constexpr int P2_WAVES = 8;
+
+// LDS-only workgroup barrier: waits for this wave's LDS traffic, not for its outstanding global loads
+// (the prefetch of the next chunk stays in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Operands of one chunk held in registers (prefetched one chunk ahead).
+struct Pre {
+  bf16x8 A[4];   // rows of W (U role) or of Q (O role) for this wave's 16 tokens, k-steps 0..3
+  bf16x8 X[2];   // O role: rows of P for this wave's 16 tokens; U role: X[0] = Ub^T of this lane's 4 tokens
+  bf16x8 KT[2];  // rows of K^T for this wave's 16 state columns, token steps 0, 1
+  float4 gt;     // G of this lane's 4 tokens
+  float GL;      // G at the chunk end
+};
+
+struct StateShared {
+  uint16_t Ss[2][VB][LDQ];   // state slice (bf16): B operand of [W; Q] S^T
+  uint16_t UhT[2][VB][LDC];  // decayed U^T, hi part   } A operands of the state update
+  uint16_t UlT[2][VB][LDC];  // decayed U^T, lo part   }
+  uint16_t UoT[2][VB][LDC];  // U^T (bf16): B operand of the output's P U
+};
+
+struct StateArgs {
+  const uint8_t* ws;
+  const uint16_t* q;
+  int c0, bos, len, nchunks, Hk, Hv, h, hk, vb;
+  float scale;
+};
+
+// The chunk loop of one wave. URole: waves 0-3 form the corrected values U = Ub - W S^T of their 16 tokens;
+// the O role (waves 4-7) forms the outputs of their 16 tokens. Both run the same barriers.
+template <bool URole, typename TOut>
+__device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, TOut* o, f32x4& S) {
+  const int l = lane_id(), wave = threadIdx.x >> 6;
+  const int tb = (wave & 3) * 16;     // this wave's token block
+  const int j = l & 15;               // value row within the slice (D layout column of [W; Q] S^T)
+  const int t0 = tb + 4 * (l >> 4);   // first of this lane's 4 tokens (D layout rows)
+  const int ncol = 16 * wave + (l & 15);
+
+  auto fetch = [&](int ci, Pre& x) {
+    const uint8_t* wsc = a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK;
+    const uint16_t* gKT = reinterpret_cast<const uint16_t*>(wsc + WS_KT);
+    const float* gG = reinterpret_cast<const float*>(wsc + WS_G);
+    if constexpr (URole) {
+      const uint16_t* gW = reinterpret_cast<const uint16_t*>(wsc + WS_W);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) x.A[kk] = frag(gW, DK, tb, 32 * kk);
+      const float* gUT = reinterpret_cast<const float*>(wsc + WS_UT);
+      x.X[0] = *reinterpret_cast<const bf16x8*>(gUT + (a.vb * VB + j) * CH + t0);  // 4 floats
+    } else {
+      const int row = min(ci * CH + tb + (l & 15), a.len - 1);  // clamp padded rows into the sequence
+      const uint16_t* qrow = a.q + ((size_t)(a.bos + row) * a.Hk + a.hk) * DK + 8 * (l >> 4);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) x.A[kk] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kk);
+      const uint16_t* gP = reinterpret_cast<const uint16_t*>(wsc + WS_P);
+      x.X[0] = frag(gP, CH, tb, 0);
+      x.X[1] = frag(gP, CH, tb, 32);
+    }
+    x.KT[0] = frag(gKT, CH, 16 * wave, 0);
+    x.KT[1] = frag(gKT, CH, 16 * wave, 32);
+    x.gt = *reinterpret_cast<const float4*>(gG + t0);
+    x.GL = gG[CH - 1];
+  };
+
+  auto as_f4 = [](bf16x8 v) { return __builtin_bit_cast(float4, v); };
+
+  auto process = [&](int ci, const Pre& cur) {
+    const int par = ci & 1;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[par][4 * (l >> 4) + i4][ncol] = f32_to_bf16(S[i4]);
+    lds_barrier();
+
+    // [W; Q] S^T for this wave's 16 tokens
+    f32x4 x = zero4();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[par][0][0], LDQ, 0, 32 * kk), x);
+    if constexpr (URole) {
+      // U = Ub - W S^T; the decayed exp(G_L - G_t) U as hi + lo bf16; U itself as bf16
+      const float4 ub4 = as_f4(cur.X[0]);
+      const float ub[4] = {ub4.x, ub4.y, ub4.z, ub4.w};
+      const float gt[4] = {cur.gt.x, cur.gt.y, cur.gt.z, cur.gt.w};
+      uint32_t hi[4], lo[4], uo[4];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const float u = ub[i4] - x[i4];
+        const float us = u * __expf(cur.GL - gt[i4]);
+        hi[i4] = f32_to_bf16(us);
+        lo[i4] = f32_to_bf16(us - bf16_to_f32((uint16_t)hi[i4]));
+        uo[i4] = f32_to_bf16(u);
+      }
+      *reinterpret_cast<uint2*>(&sh.UhT[par][j][t0]) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+      *reinterpret_cast<uint2*>(&sh.UlT[par][j][t0]) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+      *reinterpret_cast<uint2*>(&sh.UoT[par][j][t0]) = make_uint2(uo[0] | (uo[1] << 16), uo[2] | (uo[3] << 16));
+    }
+    lds_barrier();
+
+    // S <- exp(G_L) S + (decayed U)^T K for this wave's 16 columns
+    f32x4 acc = S * __expf(cur.GL);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      acc = mfma(frag(&sh.UhT[par][0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
+      acc = mfma(frag(&sh.UlT[par][0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
+    }
+    S = acc;
+    if constexpr (!URole) {
+      // O = scale exp(G_t) Q S^T + P U
+      const float gt[4] = {cur.gt.x, cur.gt.y, cur.gt.z, cur.gt.w};
+      f32x4 y;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) y[i4] = a.scale * __expf(gt[i4]) * x[i4];
+      y = mfma(cur.X[0], frag(&sh.UoT[par][0][0], LDC, 0, 0), y);
+      y = mfma(cur.X[1], frag(&sh.UoT[par][0][0], LDC, 0, 32), y);
+      const int tlen = min(CH, a.len - ci * CH);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int t = t0 + i4;
+        if (t < tlen)
+          io<TOut>::store(o + ((size_t)(a.bos + ci * CH + t) * a.Hv + a.h) * DV + a.vb * VB + j, y[i4]);
+      }
+    }
+  };
+
+  // two register buffers, alternately filled one chunk ahead (no copies between them); the fetches are
+  // unconditional (the last chunk is fetched again at the end) so every path issues the same loads and
+  // the wait before each use covers only the older buffer
+  if (a.nchunks <= 0) return;
+  const int last = a.nchunks - 1;
+  Pre b0, b1;
+  fetch(0, b0);
+  for (int ci = 0; ci < a.nchunks; ci += 2) {
+    fetch(min(ci + 1, last), b1);
+    process(ci, b0);
+    if (ci + 1 >= a.nchunks) break;
+    fetch(min(ci + 2, last), b0);
+    process(ci + 1, b1);
+  }
+}
 
 template <typename TOut>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
-    const uint8_t* __restrict__ ws, const float* __restrict__ s_in, float* __restrict__ s_out,
-    TOut* __restrict__ o, const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hv) {
-  __shared__ uint16_t Ss[VB][LDQ];   // state slice (bf16), B operand of [Qp; W] S^T
-  __shared__ uint16_t UhT[VB][LDC];  // decayed U^T, hi and lo parts: A operands of the state update
-  __shared__ uint16_t UlT[VB][LDC];
+    const uint8_t* ws, const uint16_t* q, const float* __restrict__ s_in, float* __restrict__ s_out,
+    TOut* __restrict__ o, const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hk, int Hv,
+    float scale) {
+  // (ws and q are not __restrict__: that keeps the compiler from sinking the prefetch loads below the
+  // LDS barriers, whose asm memory clobber then pins them where they are issued)
+  __shared__ StateShared sh;
 
   // XCD-aware order: the DV/VB workgroups of one (sequence, head) are `pairs` ids apart, so with
   // pairs % 8 == 0 they share an XCD and its L2 (they read the same chunk workspace).
@@ -383,128 +498,61 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   const int pair = id % pairs, vb = id / pairs;
   const int seq = pair / Hv, h = pair % Hv;
   const int l = lane_id(), wave = threadIdx.x >> 6;
+  const int ncol = 16 * wave + (l & 15);
 
-  int bos, len, c0;
+  StateArgs a;
+  a.ws = ws;
+  a.q = q;
+  a.Hk = Hk;
+  a.Hv = Hv;
+  a.h = h;
+  a.hk = h / (Hv / Hk);
+  a.vb = vb;
+  a.scale = scale;
   if (cu != nullptr) {
-    bos = cu[seq];
-    len = cu[seq + 1] - bos;
-    c0 = 0;
-    for (int s = 0; s < seq; ++s) c0 += (cu[s + 1] - cu[s] + CH - 1) / CH;
+    a.bos = cu[seq];
+    a.len = cu[seq + 1] - a.bos;
+    a.c0 = 0;
+    for (int s = 0; s < seq; ++s) a.c0 += (cu[s + 1] - cu[s] + CH - 1) / CH;
   } else {
-    bos = seq * T;
-    len = T;
-    c0 = seq * ((T + CH - 1) / CH);
+    a.bos = seq * T;
+    a.len = T;
+    a.c0 = seq * ((T + CH - 1) / CH);
   }
   // chunks past the workspace (a chunk table shorter than the sequences need) are not read
-  const int nchunks = max(0, min((len + CH - 1) / CH, n_chunks - c0));
+  a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
 
-  // state slice in the D layout of the state update: rows j = 4*(l/16)+i, columns n = 32*wave + 16*tt + l%16
-  f32x4 S[2];
+  // state slice in the D layout of the state update: rows j = 4*(l/16)+i, column ncol
+  f32x4 S;
   const size_t sbase = (((size_t)seq * Hv + h) * DV + vb * VB) * DK;
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int n = 32 * wave + 16 * tt + (l & 15);
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      S[tt][i4] = s_in != nullptr ? s_in[sbase + (size_t)(4 * (l >> 4) + i4) * DK + n] : 0.f;
-  }
+  for (int i4 = 0; i4 < 4; ++i4) S[i4] = s_in != nullptr ? s_in[sbase + (size_t)(4 * (l >> 4) + i4) * DK + ncol] : 0.f;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // settle the state loads before the pipelined loop
 
-  for (int ci = 0; ci < nchunks; ++ci) {
-    const uint8_t* wsc = ws + ((size_t)(c0 + ci) * Hv + h) * WS_CHUNK;
-    const uint16_t* gQp = reinterpret_cast<const uint16_t*>(wsc + WS_QP);
-    const uint16_t* gW = reinterpret_cast<const uint16_t*>(wsc + WS_W);
-    const uint16_t* gKT = reinterpret_cast<const uint16_t*>(wsc + WS_KT);
-    const float* gUT = reinterpret_cast<const float*>(wsc + WS_UT);
-    const uint16_t* gOT = reinterpret_cast<const uint16_t*>(wsc + WS_OT);
-    const float* gG = reinterpret_cast<const float*>(wsc + WS_G);
-    const int tlen = min(CH, len - ci * CH);
-
-    // state slice -> LDS (bf16)
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int n = 32 * wave + 16 * tt + (l & 15);
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) Ss[4 * (l >> 4) + i4][n] = f32_to_bf16(S[tt][i4]);
-    }
-    __syncthreads();
-
-    // [Qp; W] S^T for tokens 16*wave .. +15
-    f32x4 xq = zero4(), xw = zero4();
-#pragma unroll
-    for (int k0 = 0; k0 < DK; k0 += 32) {
-      const bf16x8 b = frag(&Ss[0][0], LDQ, 0, k0);
-      xq = mfma(frag(gQp, DK, 16 * wave, k0), b, xq);
-      xw = mfma(frag(gW, DK, 16 * wave, k0), b, xw);
-    }
-    const int j = l & 15;
-    const int t0 = 16 * wave + 4 * (l >> 4);
-    const float GL = gG[CH - 1];
-    {
-      // outputs O = Ol + Qp S^T
-      const uint2 ow = *reinterpret_cast<const uint2*>(gOT + (vb * VB + j) * CH + t0);
-      const float ol[4] = {__uint_as_float(ow.x << 16), __uint_as_float(ow.x & 0xffff0000u),
-                           __uint_as_float(ow.y << 16), __uint_as_float(ow.y & 0xffff0000u)};
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int t = t0 + i4;
-        if (t < tlen) io<TOut>::store(o + ((size_t)(bos + ci * CH + t) * Hv + h) * DV + vb * VB + j, ol[i4] + xq[i4]);
-      }
-      // decayed corrected values -> LDS as hi + lo bf16
-      const float4 ub = *reinterpret_cast<const float4*>(gUT + (vb * VB + j) * CH + t0);
-      const float4 gt = *reinterpret_cast<const float4*>(gG + t0);
-      const float us[4] = {(ub.x - xw[0]) * __expf(GL - gt.x), (ub.y - xw[1]) * __expf(GL - gt.y),
-                           (ub.z - xw[2]) * __expf(GL - gt.z), (ub.w - xw[3]) * __expf(GL - gt.w)};
-      uint32_t hi[4], lo[4];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        hi[i4] = f32_to_bf16(us[i4]);
-        lo[i4] = f32_to_bf16(us[i4] - bf16_to_f32((uint16_t)hi[i4]));
-      }
-      *reinterpret_cast<uint2*>(&UhT[j][t0]) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-      *reinterpret_cast<uint2*>(&UlT[j][t0]) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
-    }
-    __syncthreads();
-
-    // S = exp(G_L) S + (decayed U)^T K for columns 32*wave .. +31
-    const float dec = __expf(GL);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x4 acc = S[tt] * dec;
-      const int n0 = 32 * wave + 16 * tt;
-#pragma unroll
-      for (int k0 = 0; k0 < CH; k0 += 32) {
-        const bf16x8 kb = frag(gKT, CH, n0, k0);
-        acc = mfma(frag(&UhT[0][0], LDC, 0, k0), kb, acc);
-        acc = mfma(frag(&UlT[0][0], LDC, 0, k0), kb, acc);
-      }
-      S[tt] = acc;
-    }
-    __syncthreads();  // Ss / UhT / UlT are rewritten by the next chunk
-  }
+  if (wave < 4)
+    state_loop<true>(sh, a, o, S);
+  else
+    state_loop<false>(sh, a, o, S);
 
   if (s_out != nullptr) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int n = 32 * wave + 16 * tt + (l & 15);
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) s_out[sbase + (size_t)(4 * (l >> 4) + i4) * DK + n] = S[tt][i4];
-    }
+    for (int i4 = 0; i4 < 4; ++i4) s_out[sbase + (size_t)(4 * (l >> 4) + i4) * DK + ncol] = S[i4];
   }
 }
 
-template <typename TIn, typename TG>
+template <typename TG>
 void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const void* k, const void* v, const void* g,
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
                  const int32_t* chunk_idx, int n_seqs, int T, float scale, uint8_t* ws, hipStream_t stream) {
   dim3 grid(nchunks, Hv);
   if (gate)
-    hipLaunchKernelGGL((chunk_prep_kernel<TIn, TG, true>), grid, dim3(64 * P1_WAVES), 0, stream, (const TIn*)q,
-                       (const TIn*)k, (const TIn*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu, chunk_idx,
-                       n_seqs, T, Hk, Hv, scale, ws);
+    hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
+                       chunk_idx, n_seqs, T, Hk, Hv, scale, ws);
   else
-    hipLaunchKernelGGL((chunk_prep_kernel<TIn, TG, false>), grid, dim3(64 * P1_WAVES), 0, stream, (const TIn*)q,
-                       (const TIn*)k, (const TIn*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu, chunk_idx,
-                       n_seqs, T, Hk, Hv, scale, ws);
+    hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
+                       chunk_idx, n_seqs, T, Hk, Hv, scale, ws);
 }
 
 }  // namespace
@@ -547,14 +595,14 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
   const bool gate = A_log != nullptr;
   if (n_chunks > 0) {
     if (gb_dtype == ZGDN_F32)
-      launch_prep<bf16, float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
+      launch_prep<float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
                                N, T, scale, ws, s);
     else
-      launch_prep<bf16, bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
+      launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
                               N, T, scale, ws, s);
   }
   dim3 grid2(N * Hv * (DV / VB));
-  hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,
-                     (bf16*)o, cu_seqlens, N, n_chunks, T, Hv);
+  hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, (const uint16_t*)q,
+                     initial_state, final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hk, Hv, scale);
   return check_launch(fn);
 }
