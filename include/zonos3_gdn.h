@@ -74,6 +74,22 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
                    int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K, int V, float scale,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * One single-token step of the whole GDN block for B independent streams, fused in one launch: depthwise
+ * causal conv1d (width W == 4) over the raw q|k|v channels with a rolling history, SiLU, q/k L2-norm, the
+ * in-kernel gate, the gated delta-rule state update and the gated RMSNorm of the output. Replaces, for one
+ * new row per stream, model/src/zonos3/reference/lm.py:563-587 (and the serving layer's decode path through
+ * FLA, servers/sgl/src/zonos3_sgl/models/gdn.py:403-445).
+ *   x_qkv [B, C] with C = 2 Hk K + Hv V (q | k | v channels); z [B, Hv, V]; a, b [B, Hv]; conv_weight
+ *   [C, W] (tap 0 oldest); norm_weight [V]; out [B, Hv, V]: all of element type `dtype` (F32 or BF16).
+ *   conv_cache [B, C, W-1] (same dtype, oldest first) and state [B, Hv, V, K] (float32) are updated in place.
+ *   A_log, dt_bias: float32 [Hv]. K == V == 128, Hv / Hk in {1, 2, 4}.
+ */
+int zgdn_fused_decode_step(const void* x_qkv, const void* z, const void* a, const void* b, int dtype,
+                           const void* conv_weight, void* conv_cache, const float* A_log, const float* dt_bias,
+                           const void* norm_weight, float* state, void* out, int B, int Hk, int Hv, int K, int V,
+                           int W, float eps, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,10 +3,10 @@
 Hand-written HIP kernels behind a C ABI (``include/zonos3_gdn.h``, ``libzonos3_gdn.so``), driven from
 PyTorch-ROCm. Public surface:
 
-* ``ops``: direct ops (``recurrent_fwd``, ``decode_step``, ``chunk_fwd``).
+* ``ops``: direct ops (``recurrent_fwd``, ``decode_step``, ``chunk_fwd``, ``fused_decode_step``).
 """
 
 from . import ops  # noqa: F401
-from .ops import chunk_fwd, decode_step, recurrent_fwd  # noqa: F401
+from .ops import chunk_fwd, decode_step, fused_decode_step, recurrent_fwd  # noqa: F401
 
-__all__ = ["ops", "recurrent_fwd", "decode_step", "chunk_fwd"]
+__all__ = ["ops", "recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step"]

@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, c_size_t, _P],
     ),
+    "zgdn_fused_decode_step": (
+        c_int,
+        [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P,
+         c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -185,3 +185,48 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
         _stream(dev),
     )
     return o, final_state
+
+
+def fused_decode_step(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weight, A_log, dt_bias, eps=1e-6,
+                      scale=None):
+    """One single-token step of the whole GDN block for B streams (lm.py:563-587 for one new row each).
+
+    x_qkv [B, 2*Hk*128 + Hv*128] raw q|k|v channels; z [B, Hv, 128]; a, b [B, Hv] (raw gate inputs);
+    conv_weight [C, 4] or [C, 1, 4]; norm_weight [128] -- all bfloat16 or all float32. conv_cache [B, C, 3]
+    (same dtype, oldest first) and state [B, Hv, 128, 128] float32 are updated in place; A_log, dt_bias
+    float32 [Hv]. Returns the gated, normalised output [B, Hv, 128]."""
+    _on_gpu("x_qkv", x_qkv)
+    dev = x_qkv.device
+    _require(x_qkv.dim() == 2, f"x_qkv: expected [B, C], got {tuple(x_qkv.shape)}")
+    B, C = x_qkv.shape
+    _require(z.dim() == 3 and z.shape[0] == B, f"z: expected [B={B}, Hv, V], got {tuple(z.shape)}")
+    Hv, V = z.shape[1], z.shape[2]
+    K = V
+    _require(K == 128, f"fused_decode_step: head size {V}; the fused kernel needs 128")
+    _require((C - Hv * V) > 0 and (C - Hv * V) % (2 * K) == 0, f"x_qkv: {C} channels do not split into "
+                                                                f"q|k|v with Hv={Hv}, head size {K}")
+    Hk = (C - Hv * V) // (2 * K)
+    _require(Hv % Hk == 0 and Hv // Hk in (1, 2, 4), f"Hv/Hk = {Hv}/{Hk}: supported groups are 1, 2, 4")
+    if conv_weight.dim() == 3:
+        conv_weight = conv_weight.squeeze(1)
+    dt = x_qkv.dtype
+    for name, t, shape in (("z", z, (B, Hv, V)), ("a", a, (B, Hv)), ("b", b, (B, Hv)),
+                           ("conv_weight", conv_weight, (C, 4)), ("conv_cache", conv_cache, (B, C, 3)),
+                           ("norm_weight", norm_weight, (V,))):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == dt, f"{name}: dtype {t.dtype}, expected {dt} (the dtype of x_qkv)")
+        _require(tuple(t.shape) == shape, f"{name}: expected {list(shape)}, got {list(t.shape)}")
+    _on_gpu("state", state, dev)
+    _require(state.dtype == torch.float32 and state.shape == (B, Hv, V, K),
+             f"state: expected float32 [{B}, {Hv}, {V}, {K}]")
+    for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
+    out = torch.empty(B, Hv, V, device=dev, dtype=dt)
+    scale = K**-0.5 if scale is None else float(scale)
+    _native.call(
+        "zgdn_fused_decode_step", x_qkv.data_ptr(), z.data_ptr(), a.data_ptr(), b.data_ptr(), _code(x_qkv, "x_qkv"),
+        conv_weight.data_ptr(), conv_cache.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), norm_weight.data_ptr(),
+        state.data_ptr(), out.data_ptr(), B, Hk, Hv, K, V, 4, float(eps), scale, _stream(dev),
+    )
+    return out
