@@ -39,18 +39,22 @@ int zgdn_abi_version(void);
  * Replaces the token loop of model/src/zonos3/reference/lm.py:574-583 (S *= a; p = S.k; d = beta (v - p);
  * S += d k^T; o = S.(q scale)), which the serving layer otherwise recomputes through a 64-row chunk window
  * (servers/sgl/src/zonos3_sgl/models/gdn.py:329-355).
- *   g, beta: dtype gb_dtype (F32 or BF16); g is the log decay (alpha = exp(g)).
+ *   g, beta: dtype gb_dtype (F32 or BF16). Without A_log / dt_bias g is the log decay (alpha = exp(g)); with
+ *   them (float32 [Hv], both or neither) g is the raw gate input a and the log decay is
+ *   -exp(A_log[h]) * softplus(a + dt_bias[h]) (lm.py:572).
+ *   qk_l2norm != 0: q and k are L2-normalised in the kernel, x * rsqrt(sum x^2 + 1e-6) in fp32 (lm.py:570-571).
  *   initial_state: NULL = zeros. final_state: NULL = not written; may equal initial_state (in place).
  *   o: dtype o_dtype. K must be 64 or 128; V >= 1; Hv % Hk == 0.
  */
 int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
-                       const void* beta, int gb_dtype, const float* initial_state, float* final_state,
-                       void* o, int o_dtype, const int32_t* cu_seqlens, int n_seqs, int B, int T, int Hk,
-                       int Hv, int K, int V, float scale, void* stream);
+                       const void* beta, int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
+                       const float* initial_state, float* final_state, void* o, int o_dtype,
+                       const int32_t* cu_seqlens, int n_seqs, int B, int T, int Hk, int Hv, int K, int V,
+                       float scale, void* stream);
 
 /*
  * Bytes of workspace zgdn_chunk_fwd needs for n_chunks 64-token chunks (over all sequences) and Hv value
- * heads (73,984 bytes per chunk and head).
+ * heads (74,256 bytes per chunk and head).
  */
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
 
@@ -63,16 +67,18 @@ size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
  *   g, beta: gb_dtype. With A_log and dt_bias (float32 [Hv], both or neither) g holds the raw gate input a
  *   and the log decay is -exp(A_log[h]) * softplus(a + dt_bias[h]) (FLA use_gate_in_kernel=True,
  *   gdn.py:430-432); otherwise g is the log decay.
+ *   qk_l2norm != 0: q and k are the raw rows and are L2-normalised in the kernel (fp32 factors; the
+ *   normalised rows are never rounded to bf16), as lm.py:570-571 does before its fp32 recurrence.
  *   cu_seqlens [n_seqs+1] + chunk_indices [n_chunks, 2] (sequence, chunk within it; the table of
  *   gdn.py:49-59) for packed sequences (B == 1); otherwise n_chunks is derived from B and T.
  *   initial_state NULL = zeros; final_state NULL = not written; may equal initial_state (in place).
  *   workspace: device memory of at least zgdn_chunk_workspace_size(n_chunks, Hv) bytes.
  */
 int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g, const void* beta,
-                   int gb_dtype, const float* A_log, const float* dt_bias, const float* initial_state,
-                   float* final_state, void* o, const int32_t* cu_seqlens, const int32_t* chunk_indices,
-                   int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K, int V, float scale,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
+                   const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
+                   const int32_t* chunk_indices, int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K,
+                   int V, float scale, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * One single-token step of the whole GDN block for B independent streams, fused in one launch: depthwise
@@ -89,6 +95,46 @@ int zgdn_fused_decode_step(const void* x_qkv, const void* z, const void* a, cons
                            const void* conv_weight, void* conv_cache, const float* A_log, const float* dt_bias,
                            const void* norm_weight, float* state, void* out, int B, int Hk, int Hv, int K, int V,
                            int W, float eps, float scale, void* stream);
+
+/*
+ * Depthwise causal conv1d over packed sequences with a rolling history, optional SiLU. Replaces FLA's
+ * causal_conv1d_fwd as called at servers/sgl/src/zonos3_sgl/models/gdn.py:403-414, and the conv of
+ * model/src/zonos3/reference/lm.py:563-568 (cross-correlation, weight tap 0 oldest).
+ *   x, y [B, T, D] (packed: B == 1 with cu_seqlens [n_seqs+1] and chunk_indices [n_chunks, 2] of 64-token
+ *   chunks); weight [D, W], bias [D] or NULL; all of element type `dtype`; W <= 4.
+ *   State rows [n_seqs, D, state_width], state_width in [W-1, 4]: the raw inputs before the sequence, oldest
+ *   first (the last W-1 columns are the taps' history). lm.py keeps [D, W-1] (state_width W-1); the serving
+ *   layer keeps [N, D, W] (state_width W). final_state receives the last state_width raw inputs of
+ *   [history | x]; it may equal initial_state (in place). NULL initial_state = zeros; NULL final_state =
+ *   not written.
+ *   activation: 0 none, 1 SiLU. The conv is accumulated in fp32 and rounded to `dtype` before the
+ *   activation, the activation's result rounded again (F.conv1d then F.silu on `dtype` tensors).
+ */
+int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, int dtype,
+                           const void* initial_state, void* final_state, int state_width, void* y,
+                           const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
+                           int B, int T, int D, int W, int activation, void* stream);
+
+/*
+ * Row-wise L2 norm y = x * rsqrt(sum x^2 + eps), D <= 1024; rstd [rows] (float32) receives the factor when
+ * not NULL. Replaces FLA's l2norm_fwd (gdn.py:416-417) and lm.py:570-571 (eps 1e-6).
+ */
+int zgdn_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd, int rows, int D, float eps,
+                    void* stream);
+
+/*
+ * y = sigmoid(x) * scale elementwise. Replaces FLA's fused_beta_sigmoid_fwd (gdn.py:423) and the beta of
+ * lm.py:573.
+ */
+int zgdn_sigmoid_fwd(const void* x, int x_dtype, void* y, int y_dtype, size_t n, float scale, void* stream);
+
+/*
+ * Gated RMSNorm of the recurrent output, y = (rms_norm(x) * weight).to(dtype) * silu(g), product in fp32 then
+ * cast, one row of D <= 1024 at a time; rstd [rows] receives 1/rms when not NULL. Replaces FLA's
+ * layer_norm_gated_fwd(activation="swish", is_rms_norm=True) at gdn.py:435-445 and lm.py:584-587.
+ */
+int zgdn_gated_rmsnorm_fwd(const void* x, const void* g, const void* weight, int dtype, void* y, float* rstd,
+                           int rows, int D, float eps, void* stream);
 
 #ifdef __cplusplus
 }

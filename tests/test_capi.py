@@ -21,7 +21,9 @@ def _declared() -> set[str]:
 
 
 def test_header_declares_entry_points():
-    assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd"} <= _declared()
+    assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
+            "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
+            "zgdn_gated_rmsnorm_fwd"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -35,27 +37,56 @@ def test_library_exports_every_declared_symbol(gdn):
     assert lib.zgdn_abi_version() == 1
 
 
+def _rec_args(**over):
+    """Arguments of zgdn_recurrent_fwd by name (pointers are dummies: every call here fails validation)."""
+    p = ctypes.c_void_p(16)
+    a = dict(q=p, k=p, v=p, qkv_dtype=1, g=p, beta=p, gb_dtype=0, A_log=None, dt_bias=None, qk_l2norm=0,
+             s_in=None, s_out=None, o=p, o_dtype=1, cu=None, n_seqs=1, B=1, T=1, Hk=1, Hv=1, K=128, V=128,
+             scale=1.0, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
 def test_bad_arguments_fail_with_a_message(gdn):
     from importlib import import_module
 
     native = import_module("zonos3-mini_amd._native")
     lib = native.lib()
     p = ctypes.c_void_p(16)
-    # null pointers
-    st = lib.zgdn_recurrent_fwd(None, p, p, 1, p, p, 0, None, None, p, 1, None, 1, 1, 1, 1, 1, 128, 128, 1.0, None)
-    assert st == native.EINVAL and b"null" in lib.zgdn_last_error()
-    # grouped heads that do not divide
-    st = lib.zgdn_recurrent_fwd(p, p, p, 1, p, p, 0, None, None, p, 1, None, 1, 1, 1, 3, 4, 128, 128, 1.0, None)
-    assert st == native.EINVAL and b"multiple" in lib.zgdn_last_error()
-    # unsupported head size
-    st = lib.zgdn_recurrent_fwd(p, p, p, 1, p, p, 0, None, None, p, 1, None, 1, 1, 1, 1, 1, 96, 128, 1.0, None)
-    assert st == native.EUNSUPPORTED and b"K=96" in lib.zgdn_last_error()
-    # packed sequences need B == 1
-    st = lib.zgdn_recurrent_fwd(p, p, p, 1, p, p, 0, None, None, p, 1, p, 2, 2, 1, 1, 1, 128, 128, 1.0, None)
-    assert st == native.EINVAL and b"cu_seqlens" in lib.zgdn_last_error()
+    cases = [
+        (_rec_args(q=None), native.EINVAL, b"null"),
+        (_rec_args(Hk=3, Hv=4), native.EINVAL, b"multiple"),
+        (_rec_args(K=96), native.EUNSUPPORTED, b"K=96"),
+        (_rec_args(cu=p, n_seqs=2, B=2), native.EINVAL, b"cu_seqlens"),
+        (_rec_args(A_log=p), native.EINVAL, b"together"),
+        (_rec_args(gb_dtype=7), native.EINVAL, b"dtype"),
+    ]
+    for args, code, msg in cases:
+        assert lib.zgdn_recurrent_fwd(*args) == code
+        assert msg in lib.zgdn_last_error()
     with pytest.raises(RuntimeError, match="null"):
-        native.call("zgdn_recurrent_fwd", None, p, p, 1, p, p, 0, None, None, p, 1, None, 1, 1, 1, 1, 1, 128, 128,
-                    1.0, None)
+        native.call("zgdn_recurrent_fwd", *_rec_args(q=None))
+    # chunked prefill: head size, dtype and workspace checks
+    chunk = [p, p, p, 1, p, p, 0, None, None, 0, None, None, p, None, None, 1, 0, 1, 64, 1, 1, 128, 128, 1.0, p, 0,
+             None]
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"workspace" in lib.zgdn_last_error()
+    chunk[21] = 64  # K
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=64" in lib.zgdn_last_error()
+    chunk[21], chunk[3] = 128, 0  # fp32 q/k/v
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"bf16" in lib.zgdn_last_error()
+    assert lib.zgdn_chunk_workspace_size(64, 16) == 64 * 16 * 74256
+    # conv width, state width; row-op sizes; fused block group size
+    conv = [p, p, None, 1, None, None, 4, p, None, None, 1, 0, 1, 8, 16, 5, 1, None]
+    assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EUNSUPPORTED and b"width 5" in lib.zgdn_last_error()
+    conv[15], conv[6] = 4, 2
+    assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EINVAL and b"state width" in lib.zgdn_last_error()
+    assert lib.zgdn_l2norm_fwd(p, 1, p, 1, None, 4, 2048, 1e-6, None) == native.EUNSUPPORTED
+    assert lib.zgdn_gated_rmsnorm_fwd(p, None, p, 1, p, None, 4, 128, 1e-5, None) == native.EINVAL
+    assert lib.zgdn_sigmoid_fwd(p, 5, p, 0, 10, 1.0, None) == native.EINVAL
+    fused = [p, p, p, p, 1, p, p, p, p, p, p, p, 2, 1, 8, 128, 128, 4, 1e-6, 1.0, None]
+    assert lib.zgdn_fused_decode_step(*fused) == native.EUNSUPPORTED and b"Hv/Hk=8" in lib.zgdn_last_error()
+    fused[14], fused[17] = 2, 3
+    assert lib.zgdn_fused_decode_step(*fused) == native.EUNSUPPORTED and b"width 3" in lib.zgdn_last_error()
 
 
 def test_host_validation_refuses_cpu_tensors(gdn):

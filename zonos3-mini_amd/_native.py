@@ -27,13 +27,13 @@ SIGNATURES: dict[str, tuple] = {
     "zgdn_abi_version": (c_int, []),
     "zgdn_recurrent_fwd": (
         c_int,
-        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, _P, c_int,
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, _P, c_int,
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     ),
     "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
     "zgdn_chunk_fwd": (
         c_int,
-        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int,
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, c_size_t, _P],
     ),
     "zgdn_fused_decode_step": (
@@ -41,6 +41,13 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P,
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P],
     ),
+    "zgdn_causal_conv1d_fwd": (
+        c_int,
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
+    "zgdn_l2norm_fwd": (c_int, [_P, c_int, _P, c_int, _P, c_int, c_int, c_float, _P]),
+    "zgdn_sigmoid_fwd": (c_int, [_P, c_int, _P, c_int, c_size_t, c_float, _P]),
+    "zgdn_gated_rmsnorm_fwd": (c_int, [_P, _P, _P, c_int, _P, _P, c_int, c_int, c_float, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

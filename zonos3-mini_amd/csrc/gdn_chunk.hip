@@ -17,6 +17,11 @@
 // accumulation; the decayed U enters the state update as a hi + lo bf16 pair (two MFMAs) and the diagonal of
 // T diag(beta) is applied in fp32, which keeps the fp32 state within ~1e-4 of the exact recurrence.
 //
+// With the q/k L2-norm fused in (lm.py:570-571), q_t = rq_t cq_t and k_t = rk_t ck_t where cq, ck are the
+// raw (exactly bf16) rows and rq, rk = rsqrt(sum c^2 + 1e-6) are fp32: every factor r is folded into the
+// fp32 side of the products (A, P, TB, and the per-token factors Fq_t = s exp(G_t) rq_t and
+// Fk_t = exp(G_L - G_t) rk_t of the state pass), so the normalised q, k are never rounded to bf16.
+//
 // MFMA used: v_mfma_f32_16x16x32_bf16 (A: row lane%16, k 8*(lane/16)+0..7; B: column lane%16, same k;
 // D: row 4*(lane/16)+i, column lane%16) and v_mfma_f32_16x16x4_f32 (A[lane%16][lane/16], B[lane/16][lane%16])
 // for the fp32 block inverse.
@@ -38,11 +43,11 @@ constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
 
 // Workspace of one chunk x head (bytes).
 constexpr size_t WS_W = 0;                        // W    [64][128] bf16
-constexpr size_t WS_KT = WS_W + CH * DK * 2;      // K^T  [128][64] bf16
+constexpr size_t WS_KT = WS_W + CH * DK * 2;      // K^T  [128][64] bf16 (raw k rows: the L2 factor is in Fk)
 constexpr size_t WS_UT = WS_KT + DK * CH * 2;     // Ub^T [128][64] fp32
 constexpr size_t WS_P = WS_UT + DV * CH * 4;      // P    [64][64]  bf16
-constexpr size_t WS_G = WS_P + CH * CH * 2;       // G    [64]      fp32
-constexpr size_t WS_CHUNK = WS_G + CH * 4;        // 73,984 bytes
+constexpr size_t WS_F = WS_P + CH * CH * 2;       // Fq [64], Fk [64] fp32, then G_L (per-token factors)
+constexpr size_t WS_CHUNK = WS_F + 2 * CH * 4 + 16;  // 74,256 bytes
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
@@ -126,6 +131,8 @@ struct Prep {
   float Ys[P1_WAVES][16][20];  // per-wave 16x16 scratch of the block inverse
   float Gs[CH];
   float Bs[CH];
+  float Rq[CH];  // per-token L2 factors of q and k (1 without the fused norm)
+  float Rk[CH];
 };
 
 // Row-pair transposed store: dst[(c8 + i) * ld + r] <- (a[i], b[i]) as one 32-bit word (rows r, r + 1).
@@ -155,7 +162,7 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
-    int n_seqs, int T, int Hk, int Hv, float scale, uint8_t* __restrict__ ws) {
+    int n_seqs, int T, int Hk, int Hv, float scale, int qk_l2norm, uint8_t* __restrict__ ws) {
   __shared__ Prep sm;
   const int c = blockIdx.x, h = blockIdx.y;
   const int hk = h / (Hv / Hk);
@@ -203,9 +210,28 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     }
     sm.Gs[l] = gi;
     sm.Bs[l] = bi;
-    reinterpret_cast<float*>(wsc + WS_G)[l] = gi;
   }
   __syncthreads();
+
+  // L2 factors of the 64 q rows (threads 0-63) and k rows (64-127); read after the next barrier
+  if (tid < 2 * CH) {
+    const int r = tid & (CH - 1);
+    const uint16_t* row = tid < CH ? &sm.u.a.Qs[r][0] : &sm.u.a.Ks[r][0];
+    float ss = 0.f;
+#pragma unroll
+    for (int c8 = 0; c8 < DK; c8 += 8) {
+      const uint4 w = *reinterpret_cast<const uint4*>(row + c8);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xffff0000u);
+        ss = fmaf(lo, lo, fmaf(hi, hi, ss));
+      }
+    }
+    const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+    if (tid < CH) sm.Rq[r] = rf;
+    else sm.Rk[r] = rf;
+  }
 
   // 2. K K^T and Q K^T on the 10 lower tiles each (5 tile jobs per wave), kept in registers.
   f32x4 acc[5];
@@ -226,15 +252,15 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       int rb, cb;
       lower_tile(job % 10, rb, cb);
       const int j = cb * 16 + (l & 15);
-      const float gj = sm.Gs[j];
+      const float gj = sm.Gs[j], rkj = sm.Rk[j];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int i = rb * 16 + 4 * (l >> 4) + i4;
-        const float e = __expf(sm.Gs[i] - gj);
+        const float e = __expf(sm.Gs[i] - gj) * rkj;
         if (job < 10) {
-          sm.u.b.As[i][j] = i > j ? sm.Bs[i] * e * acc[m][i4] : 0.f;
+          sm.u.b.As[i][j] = i > j ? sm.Bs[i] * sm.Rk[i] * e * acc[m][i4] : 0.f;
         } else {
-          gP[i * CH + j] = f32_to_bf16(i >= j ? scale * e * acc[m][i4] : 0.f);
+          gP[i * CH + j] = f32_to_bf16(i >= j ? scale * sm.Rq[i] * e * acc[m][i4] : 0.f);
         }
       }
     }
@@ -243,6 +269,13 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
       const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
       gP[(rb * 16 + w / 16) * CH + cb * 16 + w % 16] = 0;
+    }
+    if (wave == 0) {
+      float* gF = reinterpret_cast<float*>(wsc + WS_F);
+      const float gl = sm.Gs[CH - 1];
+      gF[l] = scale * __expf(sm.Gs[l]) * sm.Rq[l];
+      gF[CH + l] = __expf(gl - sm.Gs[l]) * sm.Rk[l];
+      if (l == 0) gF[2 * CH] = gl;
     }
   }
   __syncthreads();
@@ -295,8 +328,8 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     const int i = e / CH, j = e % CH;
     const float t0 = i >= j ? sm.u.b.Ts[i][j] : 0.f, t1 = i >= j + 1 ? sm.u.b.Ts[i][j + 1] : 0.f;
     const float b0 = sm.Bs[j], b1 = sm.Bs[j + 1];
-    tb[m] = (uint32_t)f32_to_bf16(t0 * b0 * __expf(sm.Gs[j])) |
-            ((uint32_t)f32_to_bf16(t1 * b1 * __expf(sm.Gs[j + 1])) << 16);
+    tb[m] = (uint32_t)f32_to_bf16(t0 * b0 * sm.Rk[j] * __expf(sm.Gs[j])) |
+            ((uint32_t)f32_to_bf16(t1 * b1 * sm.Rk[j + 1] * __expf(sm.Gs[j + 1])) << 16);
     lb[m] = (uint32_t)f32_to_bf16(i > j ? t0 * b0 : 0.f) | ((uint32_t)f32_to_bf16(i > j + 1 ? t1 * b1 : 0.f) << 16);
   }
   __syncthreads();
@@ -355,7 +388,7 @@ struct Pre {
   bf16x8 A[4];   // rows of W (U role) or of Q (O role) for this wave's 16 tokens, k-steps 0..3
   bf16x8 X[2];   // O role: rows of P for this wave's 16 tokens; U role: X[0] = Ub^T of this lane's 4 tokens
   bf16x8 KT[2];  // rows of K^T for this wave's 16 state columns, token steps 0, 1
-  float4 gt;     // G of this lane's 4 tokens
+  float4 f;      // per-token factor of this lane's 4 tokens: Fk (U role) or Fq (O role)
   float GL;      // G at the chunk end
 };
 
@@ -370,7 +403,6 @@ struct StateArgs {
   const uint8_t* ws;
   const uint16_t* q;
   int c0, bos, len, nchunks, Hk, Hv, h, hk, vb;
-  float scale;
 };
 
 // The chunk loop of one wave. URole: waves 0-3 form the corrected values U = Ub - W S^T of their 16 tokens;
@@ -386,7 +418,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   auto fetch = [&](int ci, Pre& x) {
     const uint8_t* wsc = a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK;
     const uint16_t* gKT = reinterpret_cast<const uint16_t*>(wsc + WS_KT);
-    const float* gG = reinterpret_cast<const float*>(wsc + WS_G);
+    const float* gF = reinterpret_cast<const float*>(wsc + WS_F);
     if constexpr (URole) {
       const uint16_t* gW = reinterpret_cast<const uint16_t*>(wsc + WS_W);
 #pragma unroll
@@ -404,8 +436,8 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     }
     x.KT[0] = frag(gKT, CH, 16 * wave, 0);
     x.KT[1] = frag(gKT, CH, 16 * wave, 32);
-    x.gt = *reinterpret_cast<const float4*>(gG + t0);
-    x.GL = gG[CH - 1];
+    x.f = *reinterpret_cast<const float4*>(gF + (URole ? CH : 0) + t0);
+    x.GL = gF[2 * CH];
   };
 
   auto as_f4 = [](bf16x8 v) { return __builtin_bit_cast(float4, v); };
@@ -421,15 +453,15 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[par][0][0], LDQ, 0, 32 * kk), x);
     if constexpr (URole) {
-      // U = Ub - W S^T; the decayed exp(G_L - G_t) U as hi + lo bf16; U itself as bf16
+      // U = Ub - W S^T; Fk_t U (the decayed, k-normalised values) as hi + lo bf16; U itself as bf16
       const float4 ub4 = as_f4(cur.X[0]);
       const float ub[4] = {ub4.x, ub4.y, ub4.z, ub4.w};
-      const float gt[4] = {cur.gt.x, cur.gt.y, cur.gt.z, cur.gt.w};
+      const float fk[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
       uint32_t hi[4], lo[4], uo[4];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const float u = ub[i4] - x[i4];
-        const float us = u * __expf(cur.GL - gt[i4]);
+        const float us = u * fk[i4];
         hi[i4] = f32_to_bf16(us);
         lo[i4] = f32_to_bf16(us - bf16_to_f32((uint16_t)hi[i4]));
         uo[i4] = f32_to_bf16(u);
@@ -449,11 +481,11 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     }
     S = acc;
     if constexpr (!URole) {
-      // O = scale exp(G_t) Q S^T + P U
-      const float gt[4] = {cur.gt.x, cur.gt.y, cur.gt.z, cur.gt.w};
+      // O = Fq_t (raw q) S^T + P U, Fq_t = scale exp(G_t) rq_t
+      const float fq[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
       f32x4 y;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) y[i4] = a.scale * __expf(gt[i4]) * x[i4];
+      for (int i4 = 0; i4 < 4; ++i4) y[i4] = fq[i4] * x[i4];
       y = mfma(cur.X[0], frag(&sh.UoT[par][0][0], LDC, 0, 0), y);
       y = mfma(cur.X[1], frag(&sh.UoT[par][0][0], LDC, 0, 32), y);
       const int tlen = min(CH, a.len - ci * CH);
@@ -485,8 +517,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
 template <typename TOut>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
     const uint8_t* ws, const uint16_t* q, const float* __restrict__ s_in, float* __restrict__ s_out,
-    TOut* __restrict__ o, const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hk, int Hv,
-    float scale) {
+    TOut* __restrict__ o, const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hk, int Hv) {
   // (ws and q are not __restrict__: that keeps the compiler from sinking the prefetch loads below the
   // LDS barriers, whose asm memory clobber then pins them where they are issued)
   __shared__ StateShared sh;
@@ -508,7 +539,6 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   a.h = h;
   a.hk = h / (Hv / Hk);
   a.vb = vb;
-  a.scale = scale;
   if (cu != nullptr) {
     a.bos = cu[seq];
     a.len = cu[seq + 1] - a.bos;
@@ -543,16 +573,17 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 template <typename TG>
 void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const void* k, const void* v, const void* g,
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
-                 const int32_t* chunk_idx, int n_seqs, int T, float scale, uint8_t* ws, hipStream_t stream) {
+                 const int32_t* chunk_idx, int n_seqs, int T, float scale, int qk_l2norm, uint8_t* ws,
+                 hipStream_t stream) {
   dim3 grid(nchunks, Hv);
   if (gate)
     hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, T, Hk, Hv, scale, ws);
+                       chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
   else
     hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, T, Hk, Hv, scale, ws);
+                       chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
 }
 
 }  // namespace
@@ -564,7 +595,7 @@ extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
 
 extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
                               const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
-                              const float* initial_state, float* final_state, void* o,
+                              int qk_l2norm, const float* initial_state, float* final_state, void* o,
                               const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
                               int B, int T, int Hk, int Hv, int K, int V, float scale, void* workspace,
                               size_t workspace_bytes, void* stream) {
@@ -596,13 +627,13 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
   if (n_chunks > 0) {
     if (gb_dtype == ZGDN_F32)
       launch_prep<float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                               N, T, scale, ws, s);
+                               N, T, scale, qk_l2norm, ws, s);
     else
       launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                              N, T, scale, ws, s);
+                              N, T, scale, qk_l2norm, ws, s);
   }
   dim3 grid2(N * Hv * (DV / VB));
   hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, (const uint16_t*)q,
-                     initial_state, final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hk, Hv, scale);
+                     initial_state, final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hk, Hv);
   return check_launch(fn);
 }

@@ -30,8 +30,9 @@ template <typename TIn, typename TOut, typename TG, int K, int PASSES = ZGDN_REC
           int NWAVES = ZGDN_REC_NWAVES>
 __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TG* __restrict__ g,
-    const TG* __restrict__ beta, const float* s_in, float* s_out, TOut* __restrict__ o,
-    const int32_t* __restrict__ cu, int T, int Hk, int Hv, int V, float scale) {
+    const TG* __restrict__ beta, const float* __restrict__ A_log, const float* __restrict__ dt_bias, int qk_l2norm,
+    const float* s_in, float* s_out, TOut* __restrict__ o, const int32_t* __restrict__ cu, int T, int Hk, int Hv,
+    int V, float scale) {
   constexpr int LPR = K / 8;         // lanes per state row
   constexpr int RPP = 64 / LPR;      // rows per pass of a wave
   constexpr int ROWS_WAVE = RPP * PASSES;
@@ -78,10 +79,26 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
     const size_t qk_off = ((size_t)t * Hk + hk) * K;
     float4 ka = io<TIn>::load4(k + qk_off + c0), kb = io<TIn>::load4(k + qk_off + c1);
     float4 qa = io<TIn>::load4(q + qk_off + c0), qb = io<TIn>::load4(q + qk_off + c1);
-    const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-    const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+    float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    if (qk_l2norm) {  // x * rsqrt(sum x^2 + 1e-6) in fp32 (lm.py:570-571)
+      float nk = 0.f, nq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        nk = fmaf(kk[i], kk[i], nk);
+        nq = fmaf(qq[i], qq[i], nq);
+      }
+      const float rk = rsqrtf(group_sum<LPR>(nk) + 1e-6f), rq = rsqrtf(group_sum<LPR>(nq) + 1e-6f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kk[i] *= rk;
+        qq[i] *= rq;
+      }
+    }
     const size_t gh = (size_t)t * Hv + h;
-    const float alpha = __expf(io<TG>::load(g + gh));
+    const float graw = io<TG>::load(g + gh);
+    // in-kernel gate (lm.py:572): log decay = -exp(A_log) softplus(a + dt_bias); otherwise g is the log decay
+    const float alpha = __expf(A_log != nullptr ? -__expf(A_log[h]) * softplus(graw + dt_bias[h]) : graw);
     const float bt = io<TG>::load(beta + gh);
     float kq = 0.f;
 #pragma unroll
@@ -126,46 +143,52 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
   }
 }
 
+struct RecArgs {
+  const void *q, *k, *v, *g, *beta;
+  const float *A_log, *dt_bias;
+  int qk_l2norm;
+  const float* s_in;
+  float* s_out;
+  void* o;
+  const int32_t* cu;
+  int N, T, Hk, Hv, V;
+  float scale;
+};
+
 template <typename TIn, typename TOut, typename TG, int K>
-void launch(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s_in,
-            float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V, float scale,
-            hipStream_t stream) {
+void launch(const RecArgs& a, hipStream_t stream) {
   constexpr int PASSES = ZGDN_REC_PASSES, NWAVES = ZGDN_REC_NWAVES;
   constexpr int ROWS_WG = (64 / (K / 8)) * PASSES * NWAVES;
-  dim3 grid((V + ROWS_WG - 1) / ROWS_WG, Hv, N);
+  dim3 grid((a.V + ROWS_WG - 1) / ROWS_WG, a.Hv, a.N);
   hipLaunchKernelGGL((recurrent_kernel<TIn, TOut, TG, K>), grid, dim3(64 * NWAVES), 0, stream,
-                     (const TIn*)q, (const TIn*)k, (const TIn*)v, (const TG*)g, (const TG*)beta, s_in, s_out,
-                     (TOut*)o, cu, T, Hk, Hv, V, scale);
+                     (const TIn*)a.q, (const TIn*)a.k, (const TIn*)a.v, (const TG*)a.g, (const TG*)a.beta, a.A_log,
+                     a.dt_bias, a.qk_l2norm, a.s_in, a.s_out, (TOut*)a.o, a.cu, a.T, a.Hk, a.Hv, a.V, a.scale);
 }
 
 template <typename TIn, typename TOut, typename TG>
-void launch_k(int K, const void* q, const void* k, const void* v, const void* g, const void* beta,
-              const float* s_in, float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V,
-              float scale, hipStream_t stream) {
+void launch_k(int K, const RecArgs& a, hipStream_t stream) {
   if (K == 128)
-    launch<TIn, TOut, TG, 128>(q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+    launch<TIn, TOut, TG, 128>(a, stream);
   else
-    launch<TIn, TOut, TG, 64>(q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+    launch<TIn, TOut, TG, 64>(a, stream);
 }
 
 template <typename TIn, typename TOut>
-void launch_g(int gb_dtype, int K, const void* q, const void* k, const void* v, const void* g, const void* beta,
-              const float* s_in, float* s_out, void* o, const int32_t* cu, int N, int T, int Hk, int Hv, int V,
-              float scale, hipStream_t stream) {
+void launch_g(int gb_dtype, int K, const RecArgs& a, hipStream_t stream) {
   if (gb_dtype == ZGDN_F32)
-    launch_k<TIn, TOut, float>(K, q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+    launch_k<TIn, TOut, float>(K, a, stream);
   else
-    launch_k<TIn, TOut, bf16>(K, q, k, v, g, beta, s_in, s_out, o, cu, N, T, Hk, Hv, V, scale, stream);
+    launch_k<TIn, TOut, bf16>(K, a, stream);
 }
 
 }  // namespace
 }  // namespace zgdn
 
 extern "C" int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
-                                  const void* beta, int gb_dtype, const float* initial_state,
-                                  float* final_state, void* o, int o_dtype, const int32_t* cu_seqlens,
-                                  int n_seqs, int B, int T, int Hk, int Hv, int K, int V, float scale,
-                                  void* stream) {
+                                  const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
+                                  int qk_l2norm, const float* initial_state, float* final_state, void* o,
+                                  int o_dtype, const int32_t* cu_seqlens, int n_seqs, int B, int T, int Hk, int Hv,
+                                  int K, int V, float scale, void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_recurrent_fwd";
   if (!q || !k || !v || !g || !beta || !o) return fail(ZGDN_EINVAL, "%s: null tensor pointer", fn);
@@ -173,6 +196,7 @@ extern "C" int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, i
     return fail(ZGDN_EINVAL, "%s: bad sizes B=%d T=%d Hk=%d Hv=%d V=%d", fn, B, T, Hk, Hv, V);
   if (Hv % Hk) return fail(ZGDN_EINVAL, "%s: Hv=%d is not a multiple of Hk=%d", fn, Hv, Hk);
   if (K != 64 && K != 128) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d (supported: 64, 128)", fn, K);
+  if ((A_log == nullptr) != (dt_bias == nullptr)) return fail(ZGDN_EINVAL, "%s: A_log and dt_bias go together", fn);
   for (int dt : {qkv_dtype, gb_dtype, o_dtype})
     if (dt != ZGDN_F32 && dt != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: unknown dtype code %d", fn, dt);
   int N = B;
@@ -181,18 +205,16 @@ extern "C" int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, i
     if (n_seqs < 1) return fail(ZGDN_EINVAL, "%s: n_seqs=%d with cu_seqlens", fn, n_seqs);
     N = n_seqs;
   }
+  RecArgs a{q, k, v, g, beta, A_log, dt_bias, qk_l2norm, initial_state, final_state, o, cu_seqlens, N, T, Hk, Hv,
+            V, scale};
   hipStream_t s = (hipStream_t)stream;
   if (qkv_dtype == ZGDN_F32 && o_dtype == ZGDN_F32)
-    launch_g<float, float>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
-                           Hv, V, scale, s);
+    launch_g<float, float>(gb_dtype, K, a, s);
   else if (qkv_dtype == ZGDN_F32)
-    launch_g<float, bf16>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
-                          Hv, V, scale, s);
+    launch_g<float, bf16>(gb_dtype, K, a, s);
   else if (o_dtype == ZGDN_F32)
-    launch_g<bf16, float>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
-                          Hv, V, scale, s);
+    launch_g<bf16, float>(gb_dtype, K, a, s);
   else
-    launch_g<bf16, bf16>(gb_dtype, K, q, k, v, g, beta, initial_state, final_state, o, cu_seqlens, N, T, Hk,
-                         Hv, V, scale, s);
+    launch_g<bf16, bf16>(gb_dtype, K, a, s);
   return check_launch(fn);
 }

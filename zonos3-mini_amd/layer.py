@@ -1,0 +1,101 @@
+"""Drop-in for the reference model's GDN layer, ``Zonos3LM._gdn(self, x, layer, cache)``
+(``model/src/zonos3/reference/lm.py:556-602``), on the MI355X kernels.
+
+``gdn(self, x, layer, cache)`` has the method's signature and effects: it reads the layer's weights from
+``self.layers[layer].attention`` (``in_proj``, ``conv``, ``out_weight``, ``A_log``, ``dt_bias``, ``wo``),
+runs the projections through ``self._lin`` (so accent adapters still apply), replaces
+``cache.conv_state[layer]`` ([3 * inner, W - 1], x's dtype, oldest first) and ``cache.gdn_state[layer]``
+([heads, V, K] float32, value-major) with new tensors, saves the same ``gdn_*`` captures when
+``self._capture`` is set, and returns the ``wo`` projection. Bind it with ``patch(model)`` (one instance)
+or ``Zonos3LM._gdn = gdn`` (the class).
+
+Data path: one row (decode) -> the fused decode-block kernel (conv, SiLU, L2, gate, update, gated norm in
+one launch); more rows -> the conv kernel, then the chunked kernel (bf16) or the recurrent kernel (fp32),
+both with the q/k L2-norm and the gate formed in the kernel, then the gated-RMSNorm kernel.
+"""
+
+from __future__ import annotations
+
+import types
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+
+
+def _weights(a):
+    heads = a.A_log.numel()
+    hd = a.out_weight.numel()
+    conv_w = a.conv.weight
+    return heads, hd, conv_w.reshape(conv_w.shape[0], conv_w.shape[-1])
+
+
+def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
+    """``Zonos3LM._gdn`` (lm.py:556-602) on the HIP kernels: x [T, dim] -> [T, dim]."""
+    a, p = self.layers[layer].attention, f"layers.{layer}.attention."
+    heads, hd, conv_w = _weights(a)
+    inner = heads * hd
+    channels = 3 * inner
+    kernel = conv_w.shape[-1]
+    n = len(x)
+    dev, dt = x.device, x.dtype
+    projection = self._lin(p + "in_proj", x, a.in_proj.weight)
+    qkv, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
+    history = cache.conv_state.get(layer)
+    if history is None:
+        history = torch.zeros(channels, kernel - 1, dtype=dt, device=dev)
+    state = cache.gdn_state.get(layer)
+    if state is None:
+        state = torch.zeros(heads, hd, hd, dtype=torch.float32, device=dev)
+    A_log, dt_bias = a.A_log.float().contiguous(), a.dt_bias.float().contiguous()
+    conv_w = conv_w.to(dt).contiguous()
+    norm_w = a.out_weight.to(dt).contiguous()
+    capture = getattr(self, "_capture", None) is not None
+
+    if n == 1 and hd == 128 and kernel == 4 and not capture:
+        # the fused decode block updates conv history and state in place: work on fresh copies
+        new_hist = history.reshape(1, channels, kernel - 1).clone()
+        new_state = state.reshape(1, heads, hd, hd).float().clone()
+        gated = ops.fused_decode_step(qkv.contiguous(), z.reshape(1, heads, hd).contiguous(),
+                                      aa.contiguous(), b.contiguous(), conv_w, new_hist, new_state, norm_w, A_log,
+                                      dt_bias, eps=1e-5)
+        cache.conv_state[layer] = new_hist.reshape(channels, kernel - 1)
+        cache.gdn_state[layer] = new_state.reshape(heads, hd, hd)
+        return self._lin(p + "wo", gated.reshape(1, inner), a.wo.weight)
+
+    conv, new_hist = ops.causal_conv1d(qkv.contiguous().unsqueeze(0), conv_w,
+                                       initial_state=history.reshape(1, channels, kernel - 1).contiguous(),
+                                       activation="silu", state_width=kernel - 1)
+    conv = conv[0]
+    q, k, v = (part.reshape(1, n, heads, hd).contiguous() for part in conv.split(inner, -1))
+    g_raw = aa.float().reshape(1, n, heads).contiguous()
+    beta = ops.sigmoid(b.contiguous(), out_dtype=torch.float32).reshape(1, n, heads)
+    s0 = state.reshape(1, heads, hd, hd).float().contiguous()
+    kw = dict(initial_state=s0, A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=True)
+    if dt == torch.bfloat16 and hd == 128:
+        o, new_state = ops.chunk_fwd(q, k, v, g_raw, beta, **kw)
+    else:
+        o, new_state = ops.recurrent_fwd(q, k, v, g_raw, beta, out_dtype=dt, **kw)
+    recurrent = o.reshape(n, heads, hd).to(dt)
+    gated, _ = ops.gated_rmsnorm(recurrent, z.reshape(n, heads, hd).contiguous(), norm_w, eps=1e-5)
+    gated = gated.reshape(n, inner)
+    cache.conv_state[layer] = new_hist.reshape(channels, kernel - 1)
+    cache.gdn_state[layer] = new_state.reshape(heads, hd, hd)
+    if capture:
+        qn, _ = ops.l2norm(q.reshape(n, heads, hd), out_dtype=torch.float32)
+        kn, _ = ops.l2norm(k.reshape(n, heads, hd), out_dtype=torch.float32)
+        decay = torch.exp(-A_log.exp() * F.softplus(aa.float() + dt_bias))  # diagnostics only
+        for name, tensor in (
+            ("gdn_conv", conv), ("gdn_q", qn), ("gdn_k", kn), ("gdn_v", v.reshape(n, heads, hd).float()),
+            ("gdn_decay", decay), ("gdn_beta", beta.reshape(n, heads)), ("gdn_recurrent", recurrent),
+            ("gdn_gated", gated), ("gdn_state", cache.gdn_state[layer]),
+            ("gdn_conv_state", cache.conv_state[layer]),
+        ):
+            self._save(f"{name}_{layer}", tensor)
+    return self._lin(p + "wo", gated, a.wo.weight)
+
+
+def patch(model) -> None:
+    """Route one model instance's GDN layers through ``gdn``."""
+    model._gdn = types.MethodType(gdn, model)

@@ -42,6 +42,15 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+def _gate_check(A_log, dt_bias, Hv: int, device) -> None:
+    if (A_log is None) != (dt_bias is None):
+        raise RuntimeError("A_log and dt_bias go together")
+    if A_log is not None:
+        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+            _on_gpu(name, t, device)
+            _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
+
+
 def _cu_check(cu_seqlens: torch.Tensor, total: int, device) -> int:
     _on_gpu("cu_seqlens", cu_seqlens, device)
     _require(cu_seqlens.dtype == torch.int32, "cu_seqlens: must be int32")
@@ -50,13 +59,15 @@ def _cu_check(cu_seqlens: torch.Tensor, total: int, device) -> int:
 
 
 def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
-                  final_state=None):
+                  final_state=None, A_log=None, dt_bias=None, use_qk_l2norm=False, out_dtype=None):
     """Token-by-token gated delta rule (lm.py:574-583 in FLA's calling convention).
 
-    q, k [B, T, Hk, K]; v [B, T, Hv, V]; g (log decay) and beta [B, T, Hv], float32 or bfloat16;
-    initial_state [N, Hv, V, K] float32 or None (zeros); cu_seqlens int32 [N+1] with B == 1 for packed
-    sequences. ``final_state`` may name an existing float32 tensor to write (it may be ``initial_state``
-    itself: an in-place update). Returns (o [B, T, Hv, V] in v's dtype, final state or None)."""
+    q, k [B, T, Hk, K]; v [B, T, Hv, V]; g and beta [B, T, Hv], float32 or bfloat16; g is the log decay, or
+    the raw gate input when ``A_log``/``dt_bias`` (float32 [Hv]) are given (lm.py:572). ``use_qk_l2norm``
+    L2-normalises q and k in the kernel in fp32 (lm.py:570-571). initial_state [N, Hv, V, K] float32 or None
+    (zeros); cu_seqlens int32 [N+1] with B == 1 for packed sequences. ``final_state`` may name an existing
+    float32 tensor to write (it may be ``initial_state`` itself: an in-place update). Returns
+    (o [B, T, Hv, V] in ``out_dtype`` (default v's dtype), final state or None)."""
     _on_gpu("q", q)
     dev = q.device
     for name, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
@@ -71,6 +82,7 @@ def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final
     _require(q.dtype == k.dtype == v.dtype, "q, k, v: must share a dtype")
     _require(g.dtype == beta.dtype, "g, beta: must share a dtype")
     qkv_code, gb_code = _code(q, "q"), _code(g, "g")
+    _gate_check(A_log, dt_bias, Hv, dev)
     n_seqs = B
     if cu_seqlens is not None:
         _require(B == 1, "cu_seqlens: packed sequences need B == 1")
@@ -86,12 +98,12 @@ def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final
                  f"final_state: expected float32 [{n_seqs}, {Hv}, {V}, {K}]")
     elif output_final_state:
         final_state = torch.empty(n_seqs, Hv, V, K, device=dev, dtype=torch.float32)
-    o = torch.empty(B, T, Hv, V, device=dev, dtype=v.dtype)
+    o = torch.empty(B, T, Hv, V, device=dev, dtype=v.dtype if out_dtype is None else out_dtype)
     scale = K**-0.5 if scale is None else float(scale)
     _native.call(
         "zgdn_recurrent_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), qkv_code, g.data_ptr(), beta.data_ptr(),
-        gb_code, _ptr(initial_state), _ptr(final_state), o.data_ptr(), _code(o, "o"), _ptr(cu_seqlens), n_seqs,
-        B, T, Hk, Hv, K, V, scale, _stream(dev),
+        gb_code, _ptr(A_log), _ptr(dt_bias), int(bool(use_qk_l2norm)), _ptr(initial_state), _ptr(final_state),
+        o.data_ptr(), _code(o, "o"), _ptr(cu_seqlens), n_seqs, B, T, Hk, Hv, K, V, scale, _stream(dev),
     )
     return o, final_state
 
@@ -121,13 +133,14 @@ def chunk_indices_from_cu(cu_seqlens: torch.Tensor) -> torch.Tensor:
 
 
 def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
-              chunk_indices=None, A_log=None, dt_bias=None, final_state=None):
+              chunk_indices=None, A_log=None, dt_bias=None, final_state=None, use_qk_l2norm=False):
     """Chunked gated delta rule (64-token chunks, bf16 MFMA, fp32 state): the prefill core.
 
     The operator behind FLA's ``chunk_gated_delta_rule_fwd`` as the serving layer calls it
     (``servers/sgl/src/zonos3_sgl/models/gdn.py:418-434``): q, k [B, T, Hk, 128], v [B, T, Hv, 128] bf16;
     g, beta [B, T, Hv] float32 or bfloat16. With ``A_log``/``dt_bias`` (float32 [Hv]) g is the raw gate input
-    and the decay is formed in the kernel (``use_gate_in_kernel=True``). Packed sequences: B == 1,
+    and the decay is formed in the kernel (``use_gate_in_kernel=True``). ``use_qk_l2norm``: q, k are the raw
+    rows, L2-normalised in the kernel with fp32 factors (never rounded after the norm). Packed sequences: B == 1,
     ``cu_seqlens`` int32 [N+1] and optionally ``chunk_indices`` int32 [n_chunks, 2]. Returns
     (o [B, T, Hv, 128] bf16, final state [N, Hv, 128, 128] float32 or None)."""
     _on_gpu("q", q)
@@ -145,12 +158,7 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     _require(g.shape == (B, T, Hv) and beta.shape == (B, T, Hv), f"g, beta: expected [{B}, {T}, {Hv}]")
     _require(g.dtype == beta.dtype, "g, beta: must share a dtype")
     gb_code = _code(g, "g")
-    if (A_log is None) != (dt_bias is None):
-        raise RuntimeError("A_log and dt_bias go together")
-    if A_log is not None:
-        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
-            _on_gpu(name, t, dev)
-            _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
+    _gate_check(A_log, dt_bias, Hv, dev)
     n_seqs = B
     n_chunks = B * (-(-T // CHUNK))
     if cu_seqlens is not None:
@@ -180,7 +188,8 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     scale = K**-0.5 if scale is None else float(scale)
     _native.call(
         "zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), BF16, g.data_ptr(), beta.data_ptr(), gb_code,
-        _ptr(A_log), _ptr(dt_bias), _ptr(initial_state), _ptr(final_state), o.data_ptr(), _ptr(cu_seqlens),
+        _ptr(A_log), _ptr(dt_bias), int(bool(use_qk_l2norm)), _ptr(initial_state), _ptr(final_state), o.data_ptr(),
+        _ptr(cu_seqlens),
         _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, scale, workspace.data_ptr(), ws_bytes,
         _stream(dev),
     )
@@ -230,3 +239,96 @@ def fused_decode_step(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weigh
         state.data_ptr(), out.data_ptr(), B, Hk, Hv, K, V, 4, float(eps), scale, _stream(dev),
     )
     return out
+
+
+def causal_conv1d(x, weight, bias=None, initial_state=None, output_final_state=True, activation="silu",
+                  cu_seqlens=None, chunk_indices=None, state_width=None, final_state=None):
+    """Depthwise causal conv1d with a rolling history over (packed) sequences (lm.py:563-568; the operator
+    behind FLA's causal_conv1d_fwd at gdn.py:403-414).
+
+    x [B, T, D]; weight [D, W] or [D, 1, W] (tap 0 oldest); bias [D] or None; all one dtype. State rows
+    [N, D, state_width] (default W: the serving layer's [N, D, W]; lm.py keeps W-1): the raw inputs before
+    each sequence, oldest first. Returns (y [B, T, D], new state [N, D, state_width] or None); ``final_state``
+    may name the tensor to write, ``initial_state`` itself included."""
+    _on_gpu("x", x)
+    dev = x.device
+    _require(x.dim() == 3, f"x: expected [B, T, D], got {tuple(x.shape)}")
+    B, T, D = x.shape
+    if weight.dim() == 3:
+        weight = weight.squeeze(1)
+    _on_gpu("weight", weight, dev)
+    _require(weight.dim() == 2 and weight.shape[0] == D, f"weight: expected [{D}, W], got {tuple(weight.shape)}")
+    W = weight.shape[1]
+    sw = W if state_width is None else int(state_width)
+    _require(W - 1 <= sw <= 4 and 1 <= W <= 4, f"conv width {W} / state width {sw}: need W <= 4, W-1 <= sw <= 4")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None:
+            _on_gpu(name, t, dev)
+            _require(t.dtype == x.dtype, f"{name}: dtype {t.dtype}, expected {x.dtype}")
+    if bias is not None:
+        _require(bias.shape == (D,), f"bias: expected [{D}]")
+    _require(activation in (None, "silu", "swish"), f"activation {activation!r}: supported None, 'silu'")
+    n_seqs, n_chunks = B, 0
+    if cu_seqlens is not None:
+        _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        n_seqs = _cu_check(cu_seqlens, T, dev)
+        if chunk_indices is None:
+            chunk_indices = chunk_indices_from_cu(cu_seqlens)
+        _on_gpu("chunk_indices", chunk_indices, dev)
+        _require(chunk_indices.dtype == torch.int32 and chunk_indices.dim() == 2 and chunk_indices.shape[1] == 2,
+                 "chunk_indices: expected int32 [n_chunks, 2]")
+        n_chunks = chunk_indices.shape[0]
+    for name, t in (("initial_state", initial_state), ("final_state", final_state)):
+        if t is not None:
+            _on_gpu(name, t, dev)
+            _require(t.dtype == x.dtype and t.shape == (n_seqs, D, sw),
+                     f"{name}: expected {x.dtype} [{n_seqs}, {D}, {sw}], got {t.dtype} {tuple(t.shape)}")
+    if final_state is None and output_final_state:
+        final_state = torch.empty(n_seqs, D, sw, device=dev, dtype=x.dtype)
+    y = torch.empty_like(x)
+    _native.call(
+        "zgdn_causal_conv1d_fwd", x.data_ptr(), weight.data_ptr(), _ptr(bias), _code(x, "x"), _ptr(initial_state),
+        _ptr(final_state), sw, y.data_ptr(), _ptr(cu_seqlens), _ptr(chunk_indices), n_seqs, n_chunks, B, T, D, W,
+        1 if activation in ("silu", "swish") else 0, _stream(dev),
+    )
+    return y, final_state
+
+
+def l2norm(x, eps=1e-6, out_dtype=None):
+    """x * rsqrt(sum x^2 + eps) over the last dim (<= 1024); returns (y in ``out_dtype`` (default x's),
+    rstd float32 [...]) -- lm.py:570-571 / FLA l2norm_fwd (gdn.py:416-417)."""
+    _on_gpu("x", x)
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    y = torch.empty(x.shape, device=x.device, dtype=x.dtype if out_dtype is None else out_dtype)
+    rstd = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    _native.call("zgdn_l2norm_fwd", x.data_ptr(), _code(x, "x"), y.data_ptr(), _code(y, "y"), rstd.data_ptr(),
+                 rows, D, float(eps), _stream(x.device))
+    return y, rstd
+
+
+def sigmoid(x, scale=1.0, out_dtype=torch.float32):
+    """sigmoid(x) * scale elementwise (lm.py:573 / FLA fused_beta_sigmoid_fwd at gdn.py:423), in ``out_dtype``."""
+    _on_gpu("x", x)
+    y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
+    _native.call("zgdn_sigmoid_fwd", x.data_ptr(), _code(x, "x"), y.data_ptr(), _code(y, "y"), x.numel(),
+                 float(scale), _stream(x.device))
+    return y
+
+
+def gated_rmsnorm(x, g, weight, eps=1e-5):
+    """(rms_norm(x) * weight).to(dtype) * silu(g), product in fp32, over rows of the last dim (<= 1024)
+    (lm.py:584-587 / FLA layer_norm_gated_fwd at gdn.py:435-445). Returns (y, rstd float32 [...])."""
+    _on_gpu("x", x)
+    dev = x.device
+    D = x.shape[-1]
+    for name, t in (("g", g), ("weight", weight)):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == x.dtype, f"{name}: dtype {t.dtype}, expected {x.dtype}")
+    _require(g.shape == x.shape and weight.shape == (D,), "gated_rmsnorm: g like x, weight [D]")
+    rows = x.numel() // D if D else 0
+    y = torch.empty_like(x)
+    rstd = torch.empty(x.shape[:-1], device=dev, dtype=torch.float32)
+    _native.call("zgdn_gated_rmsnorm_fwd", x.data_ptr(), g.data_ptr(), weight.data_ptr(), _code(x, "x"), y.data_ptr(),
+                 rstd.data_ptr(), rows, D, float(eps), _stream(dev))
+    return y, rstd
