@@ -39,6 +39,9 @@ BF16_PEAK_TFLOPS = 2500.0
 
 DECODE = dict(B=64, H=16, K=128, V=128)
 DECODE_BYTES_PER_TOKEN_HEAD = 2 * 128 * 128 * 4 + 2 * (128 + 128) * 2 + 2 * 4  # 132,104
+# HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the same
+# counter's reading of a plain 64 MiB copy (FETCH_SIZE x 1.9993, WRITE_SIZE x 1.0): 68,259 + 65,792 KiB
+TRAFFIC_DECODE = 137_268_224
 
 
 def _args():
@@ -46,7 +49,11 @@ def _args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused"], default=None,
+                   help="run one workload only (profiling runs); the JSON line then carries that workload")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
     return p.parse_args()
 
 
@@ -155,6 +162,138 @@ def bench_prefill(torch, gdn, reps=50):
     }
 
 
+VARLEN = dict(n_seqs=32, lo=64, hi=2048, H=16, K=128, V=128)
+
+
+def varlen_lengths(torch):
+    g = torch.Generator().manual_seed(1004)
+    return torch.randint(VARLEN["lo"], VARLEN["hi"] + 1, (VARLEN["n_seqs"],), generator=g).tolist()
+
+
+def bench_varlen(torch, gdn, reps=20):
+    """Packed prefill: 32 sequences of seeded lengths in [64, 2048], one token stream with cu_seqlens,
+    per-sequence initial states ~N(0, 0.02)."""
+    from oracle import gdn_oracle as O
+
+    dev = torch.device("cuda:0")
+    lengths = varlen_lengths(torch)
+    total = sum(lengths)
+    c = VARLEN
+    d = O.make_inputs(1, total, c["H"], c["H"], c["K"], c["V"], seed=1004, dtype=torch.bfloat16, state_std=0.02,
+                      n_states=c["n_seqs"])
+    x = {n: d[n].to(dev) for n in ("q", "k", "v", "g", "beta", "s0")}
+    cu, chunks = O.chunk_tables(lengths)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    ch_t = torch.tensor(chunks, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream(dev)
+
+    def run():
+        return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t,
+                             chunk_indices=ch_t)
+
+    ms = kernel_ms(torch, stream, run, reps)
+    flops = PREFILL_FLOP_PER_CHUNK_HEAD / PREFILL["C"] * total * c["H"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"packed prefill: 32 sequences, seeded lengths in [64, 2048] (total {total} tokens), H=16, "
+                    "dk=dv=128, bf16, per-sequence initial states ~N(0,0.02), cu_seqlens",
+        "tokens_per_s": round(total / (ms * 1e-3), 1),
+        "ms": round(ms, 5),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": int(flops)},
+    }
+
+
+FUSED = dict(B=256, steps=512, Hk=8, Hv=16, K=128)
+# bytes per step: fp32 state read + write, bf16 conv cache read + write, bf16 x, z, out, bf16 a, b
+FUSED_BYTES_PER_STEP = (2 * 256 * 16 * 128 * 128 * 4 + 2 * 256 * 4096 * 3 * 2 + 256 * 4096 * 2
+                        + 2 * 256 * 16 * 128 * 2 + 2 * 256 * 16 * 2)
+
+
+def bench_fused(torch, gdn, steps_per_graph=16):
+    """Streaming decode of the whole GDN block: B=256 streams x 512 consecutive single-token steps, 8 q/k
+    heads shared by 16 v heads, conv width 4, fp32 state carried across steps, eps 1e-6."""
+    dev = torch.device("cuda:0")
+    c = FUSED
+    B, S, Hk, Hv, K = c["B"], c["steps"], c["Hk"], c["Hv"], c["K"]
+    C = 2 * Hk * K + Hv * K
+    g = torch.Generator(device=dev).manual_seed(1005)
+    bf = torch.bfloat16
+    xs = torch.randn(S, B, C, generator=g, device=dev).to(bf)
+    zs = torch.randn(S, B, Hv, K, generator=g, device=dev).to(bf)
+    as_ = torch.randn(S, B, Hv, generator=g, device=dev).to(bf)
+    bs = torch.randn(S, B, Hv, generator=g, device=dev).to(bf)
+    w = (0.2 * torch.randn(C, 4, generator=g, device=dev)).to(bf)
+    nw = (1 + 0.1 * torch.randn(K, generator=g, device=dev)).to(bf)
+    A_log = torch.zeros(Hv, device=dev)
+    dt_bias = torch.zeros(Hv, device=dev)
+    cache = torch.zeros(B, C, 3, device=dev, dtype=bf)
+    state = torch.zeros(B, Hv, K, K, device=dev)
+    stream = torch.cuda.Stream(dev)
+
+    def step(t):
+        return gdn.fused_decode_step(xs[t], zs[t], as_[t], bs[t], w, cache, state, nw, A_log, dt_bias, eps=1e-6)
+
+    graphs = []
+    with torch.cuda.stream(stream):
+        step(0)
+        torch.cuda.synchronize()
+        for gi in range(S // steps_per_graph):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                for t in range(gi * steps_per_graph, (gi + 1) * steps_per_graph):
+                    step(t)
+            graphs.append(gr)
+        for gr in graphs[:2]:
+            gr.replay()
+        cache.zero_()
+        state.zero_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for gr in graphs:
+            gr.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    k_ms = kernel_ms(torch, stream, lambda: step(7), 50)
+    achieved = FUSED_BYTES_PER_STEP / (k_ms * 1e-3) / 1e9
+    return {
+        "workload": "fused GDN block, streaming decode: B=256 streams x 512 consecutive single-token steps, "
+                    "8 q/k heads shared by 16 v heads, dk=dv=128, conv width 4 (rolling bf16 cache), SiLU, "
+                    "q/k L2-norm, in-kernel gate, gated RMSNorm eps 1e-6, fp32 state carried; 16 steps per "
+                    "HIP graph replay",
+        "tokens_per_s": round(B * S / wall, 1),
+        "ms_per_step": round(wall * 1e3 / S, 5),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "fused_decode_kernel<bf16,2>",
+                     "kernel_us": round(k_ms * 1e3, 3), "algorithmic_bytes": FUSED_BYTES_PER_STEP},
+    }
+
+
+def calibrate_copy(torch):
+    """10 device copies of 64 MiB (torch's copy kernel): the known-size reference for HBM byte counters."""
+    dev = torch.device("cuda:0")
+    a = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(10):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def cpu_baseline_prefill(torch):
+    """The CPU oracle on the whole prefill workload (B=1, T=4096, H=16, bf16 inputs), one timed run."""
+    from oracle import gdn_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    c = PREFILL
+    d = O.make_inputs(c["B"], c["T"], c["H"], c["H"], c["K"], c["V"], seed=1003, dtype=torch.bfloat16)
+    t0 = time.perf_counter()
+    O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+    sec = time.perf_counter() - t0
+    return {"value": round(c["T"] / sec, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "the whole prefill workload (T=4096, H=16) through the torch CPU restatement of the "
+                      "reference token loop, one run"}
+
+
 def cpu_baseline_decode(torch):
     from oracle import gdn_oracle as O
 
@@ -188,6 +327,12 @@ def main():
     import torch
 
     gdn = importlib.import_module("zonos3-mini_amd")
+    if a.calibrate_copy:
+        calibrate_copy(torch)
+    if a.only in ("prefill", "varlen", "fused"):
+        fn = {"prefill": bench_prefill, "varlen": bench_varlen, "fused": bench_fused}[a.only]
+        print(json.dumps({"workload_only": a.only, **fn(torch, gdn)}), flush=True)
+        return
     dec = bench_decode(torch, gdn, a.steps, a.warmup)
     line = {
         "metric": METRIC,
@@ -213,15 +358,21 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_DECODE,
             "kernel": "recurrent_kernel<bf16,bf16,float,128,1,8>",
             "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
             "algorithmic_bytes": dec["bytes_per_launch"],
         },
     }
+    if a.only == "decode":
+        print(json.dumps(line), flush=True)
+        return
     line["prefill"] = bench_prefill(torch, gdn)
+    line["varlen_prefill"] = bench_varlen(torch, gdn)
+    line["fused_decode_block"] = bench_fused(torch, gdn)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
+        line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)
     print(json.dumps(line), flush=True)
 
 
