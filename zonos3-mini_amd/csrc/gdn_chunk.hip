@@ -328,9 +328,8 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     const int i = e / CH, j = e % CH;
     const float t0 = i >= j ? sm.u.b.Ts[i][j] : 0.f, t1 = i >= j + 1 ? sm.u.b.Ts[i][j + 1] : 0.f;
     const float b0 = sm.Bs[j], b1 = sm.Bs[j + 1];
-    tb[m] = (uint32_t)f32_to_bf16(t0 * b0 * sm.Rk[j] * __expf(sm.Gs[j])) |
-            ((uint32_t)f32_to_bf16(t1 * b1 * sm.Rk[j + 1] * __expf(sm.Gs[j + 1])) << 16);
-    lb[m] = (uint32_t)f32_to_bf16(i > j ? t0 * b0 : 0.f) | ((uint32_t)f32_to_bf16(i > j + 1 ? t1 * b1 : 0.f) << 16);
+    tb[m] = pack_bf16x2(t0 * b0 * sm.Rk[j] * __expf(sm.Gs[j]), t1 * b1 * sm.Rk[j + 1] * __expf(sm.Gs[j + 1]));
+    lb[m] = pack_bf16x2(i > j ? t0 * b0 : 0.f, i > j + 1 ? t1 * b1 : 0.f);
   }
   __syncthreads();
 #pragma unroll
@@ -457,18 +456,18 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
       const float4 ub4 = as_f4(cur.X[0]);
       const float ub[4] = {ub4.x, ub4.y, ub4.z, ub4.w};
       const float fk[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
-      uint32_t hi[4], lo[4], uo[4];
+      float u[4], us[4];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const float u = ub[i4] - x[i4];
-        const float us = u * fk[i4];
-        hi[i4] = f32_to_bf16(us);
-        lo[i4] = f32_to_bf16(us - bf16_to_f32((uint16_t)hi[i4]));
-        uo[i4] = f32_to_bf16(u);
+        u[i4] = ub[i4] - x[i4];
+        us[i4] = u[i4] * fk[i4];
       }
-      *reinterpret_cast<uint2*>(&sh.UhT[par][j][t0]) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-      *reinterpret_cast<uint2*>(&sh.UlT[par][j][t0]) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
-      *reinterpret_cast<uint2*>(&sh.UoT[par][j][t0]) = make_uint2(uo[0] | (uo[1] << 16), uo[2] | (uo[3] << 16));
+      const uint32_t h01 = pack_bf16x2(us[0], us[1]), h23 = pack_bf16x2(us[2], us[3]);
+      const uint32_t l01 = pack_bf16x2(us[0] - __uint_as_float(h01 << 16), us[1] - __uint_as_float(h01 & 0xffff0000u));
+      const uint32_t l23 = pack_bf16x2(us[2] - __uint_as_float(h23 << 16), us[3] - __uint_as_float(h23 & 0xffff0000u));
+      *reinterpret_cast<uint2*>(&sh.UhT[par][j][t0]) = make_uint2(h01, h23);
+      *reinterpret_cast<uint2*>(&sh.UlT[par][j][t0]) = make_uint2(l01, l23);
+      *reinterpret_cast<uint2*>(&sh.UoT[par][j][t0]) = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
     }
     lds_barrier();
 
