@@ -7,24 +7,28 @@
 //   Ub = diag(beta) V + (T - I) diag(beta) V                        [L x V]   (diagonal exact in fp32)
 //   P  = s * lower-incl( exp(G_i - G_j) q_i.k_j )                   [L x L]
 //   U  = Ub - W S0^T                                                (the corrected values)
-//   O  = s diag(exp(G)) Q S0^T + P U
-//   S  = exp(G_L) S0 + (diag(exp(G_L - G)) U)^T K
-// Phase 1 (chunk_prep_kernel, one workgroup per chunk x head, all independent) forms W, Ub, P, K^T and G
-// into a workspace. Phase 2 (chunk_state_kernel, one workgroup per sequence x head x 16 value rows) walks the
-// chunks in order keeping its 16 x 128 slice of the fp32 state in registers: one MFMA pass over [W; Q] gives
-// W S^T and Q S^T, then the state update and the outputs' P U are a second. The next chunk's operands are
-// prefetched into registers while the current one is processed. Numerics: MFMA operands are bf16 with fp32
-// accumulation; the decayed U enters the state update as a hi + lo bf16 pair (two MFMAs) and the diagonal of
-// T diag(beta) is applied in fp32, which keeps the fp32 state within ~1e-4 of the exact recurrence.
+//   O  = s diag(exp(G)) Q S0^T + P U  =  Q' S0^T + Ob,   Q' = s diag(exp(G)) Q - P W,   Ob = P Ub
+//   S  = exp(G_L) S0 + U'^T K,   U' = diag(exp(G_L - G)) U = Ub' - W' S0^T  (Ub', W' the rows of Ub, W scaled)
+// Phase 1 (chunk_prep_kernel, one workgroup per chunk x head, all independent) forms W', Q', K^T, Ub', Ob and
+// G_L into a workspace. Phase 2 (chunk_state_kernel, one workgroup per sequence x head x 16 value rows) walks
+// the chunks in order keeping its 16 x 128 slice of the fp32 state in registers: one MFMA pass over [W'; Q']
+// gives U' and the outputs, a second the state update. Only the state pass is sequential, so the workspace is
+// stored in MFMA fragment order: every phase-2 operand load is one contiguous 1 KiB per wave (rows read
+// straight from row-major matrices cost about 2.3x as much per byte on CDNA), and the next chunk's loads are
+// issued in three groups spread over the current chunk so they overlap its MFMA and LDS work.
+// Numerics: MFMA operands are bf16 with fp32 accumulation; U' enters the state update as a hi + lo bf16 pair
+// (two MFMAs) and the diagonal of T diag(beta) is applied in fp32, which keeps the fp32 state within ~1e-4 of
+// the exact recurrence; the output path (Q', Ob, S in bf16) stays within ~1e-3 of |o|.
 //
 // With the q/k L2-norm fused in (lm.py:570-571), q_t = rq_t cq_t and k_t = rk_t ck_t where cq, ck are the
 // raw (exactly bf16) rows and rq, rk = rsqrt(sum c^2 + 1e-6) are fp32: every factor r is folded into the
-// fp32 side of the products (A, P, TB, and the per-token factors Fq_t = s exp(G_t) rq_t and
-// Fk_t = exp(G_L - G_t) rk_t of the state pass), so the normalised q, k are never rounded to bf16.
+// fp32 side of the products (A, P, the columns of T diag(beta exp(G) rk), Fq_t = s exp(G_t) rq_t and
+// Fk_t = exp(G_L - G_t) rk_t), so the normalised q, k are never rounded to bf16.
 //
 // MFMA used: v_mfma_f32_16x16x32_bf16 (A: row lane%16, k 8*(lane/16)+0..7; B: column lane%16, same k;
 // D: row 4*(lane/16)+i, column lane%16) and v_mfma_f32_16x16x4_f32 (A[lane%16][lane/16], B[lane/16][lane%16])
-// for the fp32 block inverse.
+// for the fp32 block inverse. The contraction index of the [W'; Q'] S^T pass is taken in a permuted key order
+// (kappa below) so that two 16 x 16 D tiles of W'^T computed in phase 1 are directly one A fragment.
 #include "gdn_common.h"
 
 namespace zgdn {
@@ -41,13 +45,22 @@ constexpr int LDQ = DK + 8;  // padded LDS row (bf16) of a 128-wide matrix
 constexpr int LDC = CH + 8;  // padded LDS row (bf16) of a 64-wide matrix
 constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
 
-// Workspace of one chunk x head (bytes).
-constexpr size_t WS_W = 0;                        // W    [64][128] bf16
-constexpr size_t WS_KT = WS_W + CH * DK * 2;      // K^T  [128][64] bf16 (raw k rows: the L2 factor is in Fk)
-constexpr size_t WS_UT = WS_KT + DK * CH * 2;     // Ub^T [128][64] fp32
-constexpr size_t WS_P = WS_UT + DV * CH * 4;      // P    [64][64]  bf16
-constexpr size_t WS_F = WS_P + CH * CH * 2;       // Fq [64], Fk [64] fp32, then G_L (per-token factors)
-constexpr size_t WS_CHUNK = WS_F + 2 * CH * 4 + 16;  // 74,256 bytes
+// Workspace of one chunk x head (bytes), every block in the register order of the phase-2 wave that reads it.
+// Token tile tb = 16 tokens, value block vb = 16 value rows, k-step kk = 32 keys; lane l:
+//   W'  [tb][kk][l] 8 bf16: W'[16 tb + l%16][kappa(kk, l, 0..7)]        (A fragments, U role)
+//   Q'  [tb][kk][l] 8 bf16: Q'[16 tb + l%16][kappa(kk, l, 0..7)]        (A fragments, O role)
+//   K^T [w][kk][l]  8 bf16: k[32 kk + 8 (l/16) + 0..7][16 w + l%16]     (B fragments of the state update)
+//   Ub' [vb][tb][l] 4 f32 : Ub'[16 tb + 4 (l/16) + i][16 vb + l%16]     (D tiles)
+//   Ob  [vb][tb][l] 4 bf16: Ob[16 tb + 4 (l/16) + i][16 vb + l%16]      (D tiles)
+//   G_L, then padding to a 256-byte multiple.
+// kappa(kk, l, i) = 32 kk + 4 (l/16) + i for i < 4 and 32 kk + 16 + 4 (l/16) + i - 4 for i >= 4.
+constexpr size_t WS_WP = 0;
+constexpr size_t WS_QP = WS_WP + CH * DK * 2;
+constexpr size_t WS_KT = WS_QP + CH * DK * 2;
+constexpr size_t WS_UB = WS_KT + DK * CH * 2;
+constexpr size_t WS_OB = WS_UB + CH * DV * 4;
+constexpr size_t WS_GL = WS_OB + CH * DV * 2;
+constexpr size_t WS_CHUNK = WS_GL + 256;  // 98,560 bytes
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
@@ -81,6 +94,13 @@ __device__ __forceinline__ f32x4 mm16_f32(const float* A, int lda, const float* 
   return acc;
 }
 
+// Two D tiles (keys 32 kk + 0..15 and 32 kk + 16..31, one token column per lane) as one bf16 A fragment in
+// the kappa key order.
+__device__ __forceinline__ uint4 kappa_frag(f32x4 d0, f32x4 d1) {
+  return make_uint4(pack_bf16x2(d0[0], d0[1]), pack_bf16x2(d0[2], d0[3]), pack_bf16x2(d1[0], d1[1]),
+                    pack_bf16x2(d1[2], d1[3]));
+}
+
 // Token range of chunk `c`: packed sequences (cu != nullptr, chunk index table (seq, j)) or B x T batches.
 struct ChunkRange {
   int t0, len;
@@ -109,14 +129,13 @@ __device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, cons
 
 // ----------------------------------------------------------------------------------------------- phase 1
 
-constexpr int P1_WAVES = 4;
+constexpr int P1_WAVES = 8;
+constexpr int P1_THREADS = 64 * P1_WAVES;
 
 struct Prep {
-  uint16_t KsT[DK][LDC];  // K^T (B operand of W = TB K)
-  uint16_t VsT[DV][LDC];  // V^T (B operand of Ub = LB V, and the exact diagonal term)
   union {
     struct {
-      uint16_t Qs[CH][LDQ];  // Q, K rows (operands of K K^T, Q K^T)
+      uint16_t Qs[CH][LDQ];  // raw q, k rows (operands of K K^T, Q K^T)
       uint16_t Ks[CH][LDQ];
     } a;
     struct {
@@ -124,15 +143,24 @@ struct Prep {
       float Ts[CH][LDF];  // T = (I + A)^-1 (fp32)
     } b;
     struct {
-      uint16_t TBs[CH][LDC];  // T diag(beta exp G)  (bf16)
-      uint16_t LBs[CH][LDC];  // (T - I) diag(beta)  (bf16)
+      uint16_t Rs[CH][LDC];   // R = P T diag(beta exp(G) rk)  (bf16), so that P W = R K
+      uint16_t UbT[DV][LDC];  // Ub^T (bf16): B operand of Ob = P Ub
     } c;
   } u;
+  uint16_t KsT[DK][LDC];  // raw k^T: A operand of W'^T, Q'^T; source of the K^T fragments
+  uint16_t VsT[DV][LDC];  // v^T: B operand of Ub, and the exact diagonal term
+  uint16_t Ps[CH][LDC];   // P (bf16, zero above the diagonal blocks)
+  uint16_t TBF[CH][LDC];  // diag(Fk) T diag(beta exp(G) rk)   (B operand of W'^T)
+  uint16_t TBT[CH][LDC];  // (T diag(beta exp(G) rk))^T         (B operand of R)
+  uint16_t LB[CH][LDC];   // (T - I) diag(beta)                 (A operand of Ub)
   float Ys[P1_WAVES][16][20];  // per-wave 16x16 scratch of the block inverse
   float Gs[CH];
   float Bs[CH];
+  float Bk[CH];  // beta exp(G) rk
   float Rq[CH];  // per-token L2 factors of q and k (1 without the fused norm)
   float Rk[CH];
+  float Fq[CH];  // s exp(G) rq
+  float Fk[CH];  // exp(G_L - G) rk
 };
 
 // Row-pair transposed store: dst[(c8 + i) * ld + r] <- (a[i], b[i]) as one 32-bit word (rows r, r + 1).
@@ -157,8 +185,21 @@ __device__ __forceinline__ void lower_tile(int t, int& rb, int& cb) {
   cb = t - rb * (rb + 1) / 2;
 }
 
+// Zero the 6 blocks above the diagonal of a 64x64 bf16 matrix with 16x16 blocks.
+__device__ __forceinline__ void zero_upper_blocks(uint16_t* m, int ld) {
+  for (int e = threadIdx.x; e < 6 * 256; e += P1_THREADS) {
+    const int t = e / 256, w = e % 256;
+    const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
+    const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+    m[(rb * 16 + w / 16) * ld + cb * 16 + w % 16] = 0;
+  }
+}
+
+// Contraction length over tokens for token tile tb of a lower-triangular left operand.
+__device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
+
 template <typename TG, bool GATE>
-__global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
+__global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
@@ -171,8 +212,8 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
   uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
 
   // 1. rows of q, k, v -> LDS as row pairs (zeros past the chunk end): Q, K row-major, K^T and V^T.
-  for (int item = tid; item < (CH / 2) * (DK / 8); item += 64 * P1_WAVES) {
-    const int p = item % (CH / 2), c8 = (item / (CH / 2)) * 8;
+  {
+    const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // 32 row pairs x 16 column groups
     const int r0 = 2 * p, r1 = 2 * p + 1;
     const uint4 z = make_uint4(0, 0, 0, 0);
     uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
@@ -195,7 +236,7 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     store_pair_t(&sm.KsT[0][0], LDC, c8, r0, k0, k1);
     store_pair_t(&sm.VsT[0][0], LDC, c8, r0, v0, v1);
   }
-  if (wave == 0) {
+  if (wave == P1_WAVES - 1) {
     float gi = 0.f, bi = 0.f;
     if (l < cr.len) {
       const size_t gh = (size_t)(cr.t0 + l) * Hv + h;
@@ -213,7 +254,7 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // L2 factors of the 64 q rows (threads 0-63) and k rows (64-127); read after the next barrier
+  // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127)
   if (tid < 2 * CH) {
     const int r = tid & (CH - 1);
     const uint16_t* row = tid < CH ? &sm.u.a.Qs[r][0] : &sm.u.a.Ks[r][0];
@@ -229,26 +270,35 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       }
     }
     const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-    if (tid < CH) sm.Rq[r] = rf;
-    else sm.Rk[r] = rf;
+    const float gr = sm.Gs[r];
+    if (tid < CH) {
+      sm.Rq[r] = rf;
+      sm.Fq[r] = scale * __expf(gr) * rf;
+    } else {
+      sm.Rk[r] = rf;
+      sm.Fk[r] = __expf(sm.Gs[CH - 1] - gr) * rf;
+      sm.Bk[r] = sm.Bs[r] * __expf(gr) * rf;
+    }
   }
 
-  // 2. K K^T and Q K^T on the 10 lower tiles each (5 tile jobs per wave), kept in registers.
-  f32x4 acc[5];
+  // 2. K K^T and Q K^T on the 10 lower tiles each (20 tile jobs over 8 waves), kept in registers.
+  f32x4 acc[3];
 #pragma unroll
-  for (int m = 0; m < 5; ++m) {
+  for (int m = 0; m < 3; ++m) {
     const int job = wave + P1_WAVES * m;
-    int rb, cb;
-    lower_tile(job % 10, rb, cb);
-    const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
-    acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
+    acc[m] = zero4();
+    if (job < 20) {
+      int rb, cb;
+      lower_tile(job % 10, rb, cb);
+      const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
+      acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
+    }
   }
-  __syncthreads();  // As / Ts overwrite Qs / Ks
-  {
-    uint16_t* gP = reinterpret_cast<uint16_t*>(wsc + WS_P);
+  __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
 #pragma unroll
-    for (int m = 0; m < 5; ++m) {
-      const int job = wave + P1_WAVES * m;
+  for (int m = 0; m < 3; ++m) {
+    const int job = wave + P1_WAVES * m;
+    if (job < 20) {
       int rb, cb;
       lower_tile(job % 10, rb, cb);
       const int j = cb * 16 + (l & 15);
@@ -257,27 +307,14 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
       for (int i4 = 0; i4 < 4; ++i4) {
         const int i = rb * 16 + 4 * (l >> 4) + i4;
         const float e = __expf(sm.Gs[i] - gj) * rkj;
-        if (job < 10) {
+        if (job < 10)
           sm.u.b.As[i][j] = i > j ? sm.Bs[i] * sm.Rk[i] * e * acc[m][i4] : 0.f;
-        } else {
-          gP[i * CH + j] = f32_to_bf16(i >= j ? scale * sm.Rq[i] * e * acc[m][i4] : 0.f);
-        }
+        else
+          sm.Ps[i][j] = f32_to_bf16(i >= j ? scale * sm.Rq[i] * e * acc[m][i4] : 0.f);
       }
     }
-    for (int e = tid; e < 6 * 256; e += 64 * P1_WAVES) {  // zero upper blocks of P
-      const int t = e / 256, w = e % 256;
-      const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
-      const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-      gP[(rb * 16 + w / 16) * CH + cb * 16 + w % 16] = 0;
-    }
-    if (wave == 0) {
-      float* gF = reinterpret_cast<float*>(wsc + WS_F);
-      const float gl = sm.Gs[CH - 1];
-      gF[l] = scale * __expf(sm.Gs[l]) * sm.Rq[l];
-      gF[CH + l] = __expf(gl - sm.Gs[l]) * sm.Rk[l];
-      if (l == 0) gF[2 * CH] = gl;
-    }
   }
+  zero_upper_blocks(&sm.Ps[0][0], LDC);
   __syncthreads();
 
   // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
@@ -320,57 +357,92 @@ __global__ __launch_bounds__(64 * P1_WAVES) void chunk_prep_kernel(
     __syncthreads();
   }
 
-  // 3c. TB = T diag(beta exp G) and LB = (T - I) diag(beta) in bf16 (through registers: they overwrite A, T).
-  uint32_t tb[CH * CH / (64 * P1_WAVES) / 2], lb[CH * CH / (64 * P1_WAVES) / 2];
-#pragma unroll
-  for (int m = 0; m < CH * CH / (64 * P1_WAVES) / 2; ++m) {
-    const int e = 2 * (tid + 64 * P1_WAVES * m);  // two adjacent columns
-    const int i = e / CH, j = e % CH;
+  // 3c. the bf16 forms of T: TBF = diag(Fk) T diag(Bk), TBT = (T diag(Bk))^T, LB = (T - I) diag(beta).
+  for (int e = tid; e < CH * CH / 2; e += P1_THREADS) {
+    const int i = (2 * e) / CH, j = (2 * e) % CH;  // two adjacent columns j, j + 1 of row i
     const float t0 = i >= j ? sm.u.b.Ts[i][j] : 0.f, t1 = i >= j + 1 ? sm.u.b.Ts[i][j + 1] : 0.f;
-    const float b0 = sm.Bs[j], b1 = sm.Bs[j + 1];
-    tb[m] = pack_bf16x2(t0 * b0 * sm.Rk[j] * __expf(sm.Gs[j]), t1 * b1 * sm.Rk[j + 1] * __expf(sm.Gs[j + 1]));
-    lb[m] = pack_bf16x2(i > j ? t0 * b0 : 0.f, i > j + 1 ? t1 * b1 : 0.f);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < CH * CH / (64 * P1_WAVES) / 2; ++m) {
-    const int e = 2 * (tid + 64 * P1_WAVES * m);
-    const int i = e / CH, j = e % CH;
-    *reinterpret_cast<uint32_t*>(&sm.u.c.TBs[i][j]) = tb[m];
-    *reinterpret_cast<uint32_t*>(&sm.u.c.LBs[i][j]) = lb[m];
+    const float tb0 = t0 * sm.Bk[j], tb1 = t1 * sm.Bk[j + 1];
+    const float fk = sm.Fk[i];
+    *reinterpret_cast<uint32_t*>(&sm.TBF[i][j]) = pack_bf16x2(fk * tb0, fk * tb1);
+    *reinterpret_cast<uint32_t*>(&sm.LB[i][j]) = pack_bf16x2(i > j ? t0 * sm.Bs[j] : 0.f,
+                                                              i > j + 1 ? t1 * sm.Bs[j + 1] : 0.f);
+    sm.TBT[j][i] = f32_to_bf16(tb0);
+    sm.TBT[j + 1][i] = f32_to_bf16(tb1);
   }
   __syncthreads();
 
-  // 4. W = TB K, Ub = beta V + LB V (32 tiles each); K^T to the workspace.
+  // 4. W' (as A fragments), Ub' (+ Ub^T in LDS), R = P T diag(Bk), and the K^T fragments.
   {
-    uint16_t* gW = reinterpret_cast<uint16_t*>(wsc + WS_W);
-    float* gUT = reinterpret_cast<float*>(wsc + WS_UT);
-    for (int job = wave; job < 64; job += P1_WAVES) {
-      const int which = job >> 5, t = job & 31;
-      const int rb = t >> 3, nb = t & 7;
-      const int kend = rb < 2 ? 32 : 64;  // TB and LB vanish above the block diagonal
-      const int n = nb * 16 + (l & 15);
-      const int i0 = rb * 16 + 4 * (l >> 4);
-      if (which == 0) {
-        const f32x4 w = tile_mm(&sm.u.c.TBs[0][0], LDC, rb * 16, &sm.KsT[0][0], LDC, nb * 16, kend, zero4());
+    uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
+    for (int job = wave; job < 16; job += P1_WAVES) {  // (token tile, k-step): W'^T = K^T TBF^T
+      const int tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
+      const f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
+      const f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
+      gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+    }
+    float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
+    for (int job = wave; job < 32; job += P1_WAVES) {  // (token tile, value block): Ub = beta V + LB V
+      const int tb = job >> 3, vb = job & 7;
+      const f32x4 u = tile_mm(&sm.LB[0][0], LDC, 16 * tb, &sm.VsT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+      const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
+      const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
+      float ub[4];
+      ub[0] = fmaf(sm.Bs[i0], __uint_as_float(vv.x << 16), u[0]);
+      ub[1] = fmaf(sm.Bs[i0 + 1], __uint_as_float(vv.x & 0xffff0000u), u[1]);
+      ub[2] = fmaf(sm.Bs[i0 + 2], __uint_as_float(vv.y << 16), u[2]);
+      ub[3] = fmaf(sm.Bs[i0 + 3], __uint_as_float(vv.y & 0xffff0000u), u[3]);
+      gU[(vb * 4 + tb) * 64 + l] =
+          make_float4(sm.Fk[i0] * ub[0], sm.Fk[i0 + 1] * ub[1], sm.Fk[i0 + 2] * ub[2], sm.Fk[i0 + 3] * ub[3]);
+      *reinterpret_cast<uint2*>(&sm.u.c.UbT[n][i0]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
+    }
+    for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
+      int rb, cb;
+      lower_tile(job, rb, cb);
+      const f32x4 r = tile_mm(&sm.Ps[0][0], LDC, 16 * rb, &sm.TBT[0][0], LDC, 16 * cb, tri_kend(rb), zero4());
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) gW[(i0 + i4) * DK + n] = f32_to_bf16(w[i4]);
-      } else {
-        const f32x4 u = tile_mm(&sm.u.c.LBs[0][0], LDC, rb * 16, &sm.VsT[0][0], LDC, nb * 16, kend, zero4());
-        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
-        float4 o;
-        o.x = fmaf(sm.Bs[i0], __uint_as_float(vv.x << 16), u[0]);
-        o.y = fmaf(sm.Bs[i0 + 1], __uint_as_float(vv.x & 0xffff0000u), u[1]);
-        o.z = fmaf(sm.Bs[i0 + 2], __uint_as_float(vv.y << 16), u[2]);
-        o.w = fmaf(sm.Bs[i0 + 3], __uint_as_float(vv.y & 0xffff0000u), u[3]);
-        *reinterpret_cast<float4*>(gUT + n * CH + i0) = o;
-      }
+      for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[16 * rb + 4 * (l >> 4) + i4][16 * cb + (l & 15)] = f32_to_bf16(r[i4]);
     }
+    zero_upper_blocks(&sm.u.c.Rs[0][0], LDC);
     uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
-    for (int e = tid; e < DK * CH / 8; e += 64 * P1_WAVES) {
-      const int n = e / (CH / 8), t8 = (e % (CH / 8)) * 8;
-      gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[n][t8]);
+    for (int e = tid; e < DK * CH / 8; e += P1_THREADS) {  // fragment f = 2 w + kk, lane ll
+      const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
+      gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[16 * w + (ll & 15)][32 * kk + 8 * (ll >> 4)]);
     }
+  }
+  __syncthreads();
+
+  // 5. Q' = Fq q - R K (as A fragments) and Ob = P Ub (D tiles, bf16); G_L.
+  {
+    uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
+    for (int job = wave; job < 16; job += P1_WAVES) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
+      const int tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
+      f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
+      f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
+      const int tok = 16 * tb + (l & 15);
+      uint2 c0 = make_uint2(0, 0), c1 = make_uint2(0, 0);
+      if (tok < cr.len) {  // raw q row (L2-resident since step 1)
+        const uint16_t* qrow = q + ((size_t)(cr.t0 + tok) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
+        c0 = *reinterpret_cast<const uint2*>(qrow);
+        c1 = *reinterpret_cast<const uint2*>(qrow + 16);
+      }
+      const float fq = sm.Fq[tok];
+      d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
+      d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
+      d0[2] = fmaf(fq, __uint_as_float(c0.y << 16), -d0[2]);
+      d0[3] = fmaf(fq, __uint_as_float(c0.y & 0xffff0000u), -d0[3]);
+      d1[0] = fmaf(fq, __uint_as_float(c1.x << 16), -d1[0]);
+      d1[1] = fmaf(fq, __uint_as_float(c1.x & 0xffff0000u), -d1[1]);
+      d1[2] = fmaf(fq, __uint_as_float(c1.y << 16), -d1[2]);
+      d1[3] = fmaf(fq, __uint_as_float(c1.y & 0xffff0000u), -d1[3]);
+      gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+    }
+    uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
+    for (int job = wave; job < 32; job += P1_WAVES) {  // (token tile, value block): Ob = P Ub
+      const int tb = job >> 3, vb = job & 7;
+      const f32x4 y = tile_mm(&sm.Ps[0][0], LDC, 16 * tb, &sm.u.c.UbT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+      gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    }
+    if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
   }
 }
 
@@ -384,141 +456,141 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 // Operands of one chunk held in registers (prefetched one chunk ahead).
 struct Pre {
-  bf16x8 A[4];   // rows of W (U role) or of Q (O role) for this wave's 16 tokens, k-steps 0..3
-  bf16x8 X[2];   // O role: rows of P for this wave's 16 tokens; U role: X[0] = Ub^T of this lane's 4 tokens
-  bf16x8 KT[2];  // rows of K^T for this wave's 16 state columns, token steps 0, 1
-  float4 f;      // per-token factor of this lane's 4 tokens: Fk (U role) or Fq (O role)
+  bf16x8 A[4];   // W' (U role) or Q' (O role) fragments of this wave's 16 tokens, k-steps 0..3
+  bf16x8 KT[2];  // K^T fragments of this wave's 16 state columns, token steps 0, 1
+  uint4 X;       // U role: Ub' (4 fp32); O role: Ob (4 bf16 in .x, .y)
   float GL;      // G at the chunk end
 };
 
+// Single buffers suffice: each is rewritten only after a barrier that every reader of it has passed.
 struct StateShared {
-  uint16_t Ss[2][VB][LDQ];   // state slice (bf16): B operand of [W; Q] S^T
-  uint16_t UhT[2][VB][LDC];  // decayed U^T, hi part   } A operands of the state update
-  uint16_t UlT[2][VB][LDC];  // decayed U^T, lo part   }
-  uint16_t UoT[2][VB][LDC];  // U^T (bf16): B operand of the output's P U
+  uint16_t Ss[VB][LDQ];   // state slice (bf16), key columns at positions pi(key): B operand of [W'; Q'] S^T
+  uint16_t UhT[VB][LDC];  // U'^T, hi part   } A operands of the state update
+  uint16_t UlT[VB][LDC];  // U'^T, lo part   }
 };
 
 struct StateArgs {
   const uint8_t* ws;
-  const uint16_t* q;
-  int c0, bos, len, nchunks, Hk, Hv, h, hk, vb;
+  int c0, bos, len, nchunks, Hv, h, vb;
 };
 
-// The chunk loop of one wave. URole: waves 0-3 form the corrected values U = Ub - W S^T of their 16 tokens;
-// the O role (waves 4-7) forms the outputs of their 16 tokens. Both run the same barriers.
+// The chunk loop of one wave. URole: waves 0-3 form U' = Ub' - W' S^T of their 16 tokens; the O role
+// (waves 4-7) forms the outputs O = Ob + Q' S^T of their 16 tokens. Both run the same barriers and each
+// wave updates 16 columns of the state slice.
 template <bool URole, typename TOut>
 __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, TOut* o, f32x4& S) {
   const int l = lane_id(), wave = threadIdx.x >> 6;
-  const int tb = (wave & 3) * 16;     // this wave's token block
-  const int j = l & 15;               // value row within the slice (D layout column of [W; Q] S^T)
-  const int t0 = tb + 4 * (l >> 4);   // first of this lane's 4 tokens (D layout rows)
-  const int ncol = 16 * wave + (l & 15);
+  const int tb = wave & 3;               // this wave's token tile
+  const int j = l & 15;                  // value row within the slice (D layout column of [W'; Q'] S^T)
+  const int t0 = 16 * tb + 4 * (l >> 4);  // first of this lane's 4 tokens (D layout rows)
+  // position of key column 16 wave + l%16 in Ss, the inverse of kappa
+  const int pcol = 32 * (wave >> 1) + 8 * ((l & 15) >> 2) + 4 * (wave & 1) + (l & 3);
 
-  auto fetch = [&](int ci, Pre& x) {
-    const uint8_t* wsc = a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK;
-    const uint16_t* gKT = reinterpret_cast<const uint16_t*>(wsc + WS_KT);
-    const float* gF = reinterpret_cast<const float*>(wsc + WS_F);
+  auto chunk_ws = [&](int ci) { return a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK; };
+  // per-lane byte offsets inside a chunk's workspace (32-bit, so each load is a uniform base + lane offset)
+  const uint32_t offA = (uint32_t)(URole ? WS_WP : WS_QP) + (uint32_t)(tb * 4 * 64 + l) * 16u;
+  const uint32_t offX = URole ? (uint32_t)WS_UB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 16u
+                              : (uint32_t)WS_OB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 8u;
+  const uint32_t offK = (uint32_t)WS_KT + (uint32_t)(wave * 2 * 64 + l) * 16u;
+  auto ld16 = [](const uint8_t* w, uint32_t off) { return *reinterpret_cast<const bf16x8*>(w + off); };
+  // the next chunk's loads in groups spread over the phases of the current chunk
+  auto fetch1 = [&](const uint8_t* w, Pre& x) {
+    x.A[0] = ld16(w, offA);
+    x.A[1] = ld16(w, offA + 1024u);
+    x.GL = *reinterpret_cast<const float*>(w + WS_GL);
+  };
+  auto fetch2 = [&](const uint8_t* w, Pre& x) {
+    x.A[2] = ld16(w, offA + 2048u);
+    x.A[3] = ld16(w, offA + 3072u);
     if constexpr (URole) {
-      const uint16_t* gW = reinterpret_cast<const uint16_t*>(wsc + WS_W);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) x.A[kk] = frag(gW, DK, tb, 32 * kk);
-      const float* gUT = reinterpret_cast<const float*>(wsc + WS_UT);
-      x.X[0] = *reinterpret_cast<const bf16x8*>(gUT + (a.vb * VB + j) * CH + t0);  // 4 floats
+      x.X = *reinterpret_cast<const uint4*>(w + offX);
     } else {
-      const int row = min(ci * CH + tb + (l & 15), a.len - 1);  // clamp padded rows into the sequence
-      const uint16_t* qrow = a.q + ((size_t)(a.bos + row) * a.Hk + a.hk) * DK + 8 * (l >> 4);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) x.A[kk] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kk);
-      const uint16_t* gP = reinterpret_cast<const uint16_t*>(wsc + WS_P);
-      x.X[0] = frag(gP, CH, tb, 0);
-      x.X[1] = frag(gP, CH, tb, 32);
+      const uint2 ob = *reinterpret_cast<const uint2*>(w + offX);
+      x.X = make_uint4(ob.x, ob.y, 0, 0);
     }
-    x.KT[0] = frag(gKT, CH, 16 * wave, 0);
-    x.KT[1] = frag(gKT, CH, 16 * wave, 32);
-    x.f = *reinterpret_cast<const float4*>(gF + (URole ? CH : 0) + t0);
-    x.GL = gF[2 * CH];
+  };
+  auto fetch3 = [&](const uint8_t* w, Pre& x) {
+    x.KT[0] = ld16(w, offK);
+    x.KT[1] = ld16(w, offK + 1024u);
   };
 
-  auto as_f4 = [](bf16x8 v) { return __builtin_bit_cast(float4, v); };
-
-  auto process = [&](int ci, const Pre& cur) {
-    const int par = ci & 1;
+  auto process = [&](int ci, const Pre& cur, const uint8_t* wn, Pre& nxt) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[par][4 * (l >> 4) + i4][ncol] = f32_to_bf16(S[i4]);
+    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[4 * (l >> 4) + i4][pcol] = f32_to_bf16(S[i4]);
+    fetch1(wn, nxt);
     lds_barrier();
 
-    // [W; Q] S^T for this wave's 16 tokens
+    // [W'; Q'] S^T for this wave's 16 tokens
     f32x4 x = zero4();
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[par][0][0], LDQ, 0, 32 * kk), x);
+    for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk), x);
+    fetch2(wn, nxt);
+    fetch3(wn, nxt);
+    asm volatile("" ::: "memory");  // keeps the loads ahead of the output stores and the barrier
     if constexpr (URole) {
-      // U = Ub - W S^T; Fk_t U (the decayed, k-normalised values) as hi + lo bf16; U itself as bf16
-      const float4 ub4 = as_f4(cur.X[0]);
-      const float ub[4] = {ub4.x, ub4.y, ub4.z, ub4.w};
-      const float fk[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
-      float u[4], us[4];
+      // U' = Ub' - W' S^T as hi + lo bf16
+      const float ub[4] = {__uint_as_float(cur.X.x), __uint_as_float(cur.X.y), __uint_as_float(cur.X.z),
+                           __uint_as_float(cur.X.w)};
+      float u[4];
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u[i4] = ub[i4] - x[i4];
-        us[i4] = u[i4] * fk[i4];
-      }
-      const uint32_t h01 = pack_bf16x2(us[0], us[1]), h23 = pack_bf16x2(us[2], us[3]);
-      const uint32_t l01 = pack_bf16x2(us[0] - __uint_as_float(h01 << 16), us[1] - __uint_as_float(h01 & 0xffff0000u));
-      const uint32_t l23 = pack_bf16x2(us[2] - __uint_as_float(h23 << 16), us[3] - __uint_as_float(h23 & 0xffff0000u));
-      *reinterpret_cast<uint2*>(&sh.UhT[par][j][t0]) = make_uint2(h01, h23);
-      *reinterpret_cast<uint2*>(&sh.UlT[par][j][t0]) = make_uint2(l01, l23);
-      *reinterpret_cast<uint2*>(&sh.UoT[par][j][t0]) = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
-    }
-    lds_barrier();
-
-    // S <- exp(G_L) S + (decayed U)^T K for this wave's 16 columns
-    f32x4 acc = S * __expf(cur.GL);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      acc = mfma(frag(&sh.UhT[par][0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
-      acc = mfma(frag(&sh.UlT[par][0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
-    }
-    S = acc;
-    if constexpr (!URole) {
-      // O = Fq_t (raw q) S^T + P U, Fq_t = scale exp(G_t) rq_t
-      const float fq[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
-      f32x4 y;
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) y[i4] = fq[i4] * x[i4];
-      y = mfma(cur.X[0], frag(&sh.UoT[par][0][0], LDC, 0, 0), y);
-      y = mfma(cur.X[1], frag(&sh.UoT[par][0][0], LDC, 0, 32), y);
+      for (int i4 = 0; i4 < 4; ++i4) u[i4] = ub[i4] - x[i4];
+      const uint32_t h01 = pack_bf16x2(u[0], u[1]), h23 = pack_bf16x2(u[2], u[3]);
+      const uint32_t l01 = pack_bf16x2(u[0] - __uint_as_float(h01 << 16), u[1] - __uint_as_float(h01 & 0xffff0000u));
+      const uint32_t l23 = pack_bf16x2(u[2] - __uint_as_float(h23 << 16), u[3] - __uint_as_float(h23 & 0xffff0000u));
+      *reinterpret_cast<uint2*>(&sh.UhT[j][t0]) = make_uint2(h01, h23);
+      *reinterpret_cast<uint2*>(&sh.UlT[j][t0]) = make_uint2(l01, l23);
+    } else {
+      // O = Ob + Q' S^T
+      const float ob[4] = {__uint_as_float(cur.X.x << 16), __uint_as_float(cur.X.x & 0xffff0000u),
+                           __uint_as_float(cur.X.y << 16), __uint_as_float(cur.X.y & 0xffff0000u)};
       const int tlen = min(CH, a.len - ci * CH);
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int t = t0 + i4;
         if (t < tlen)
-          io<TOut>::store(o + ((size_t)(a.bos + ci * CH + t) * a.Hv + a.h) * DV + a.vb * VB + j, y[i4]);
+          io<TOut>::store(o + ((size_t)(a.bos + ci * CH + t) * a.Hv + a.h) * DV + a.vb * VB + j, ob[i4] + x[i4]);
       }
     }
+    lds_barrier();
+
+    // S <- exp(G_L) S + U'^T K for this wave's 16 columns
+    f32x4 acc = S * __expf(cur.GL);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      acc = mfma(frag(&sh.UhT[0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
+      acc = mfma(frag(&sh.UlT[0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
+    }
+    S = acc;
   };
 
-  // two register buffers, alternately filled one chunk ahead (no copies between them); the fetches are
-  // unconditional (the last chunk is fetched again at the end) so every path issues the same loads and
-  // the wait before each use covers only the older buffer
+  // two register buffers, alternately filled one chunk ahead (no copies between them). The fetches are
+  // unconditional (the last chunk is fetched again at the end) so every path issues the same loads, and the
+  // first chunk is peeled so that the loop is entered with the same loads in flight as at its back edge
+  // (which keeps the compiler's wait counts at the loop head from covering the prefetch).
   if (a.nchunks <= 0) return;
   const int last = a.nchunks - 1;
   Pre b0, b1;
-  fetch(0, b0);
-  for (int ci = 0; ci < a.nchunks; ci += 2) {
-    fetch(min(ci + 1, last), b1);
-    process(ci, b0);
-    if (ci + 1 >= a.nchunks) break;
-    fetch(min(ci + 2, last), b0);
-    process(ci + 1, b1);
+  {
+    const uint8_t* w0 = chunk_ws(0);
+    fetch1(w0, b0);
+    fetch2(w0, b0);
+    fetch3(w0, b0);
   }
+  process(0, b0, chunk_ws(min(1, last)), b1);
+  int ci = 1;
+  for (; ci + 1 < a.nchunks; ci += 2) {
+    process(ci, b1, chunk_ws(ci + 1), b0);
+    process(ci + 1, b0, chunk_ws(min(ci + 2, last)), b1);
+  }
+  if (ci < a.nchunks) process(ci, b1, chunk_ws(ci), b0);
 }
 
 template <typename TOut>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
-    const uint8_t* ws, const uint16_t* q, const float* __restrict__ s_in, float* __restrict__ s_out,
-    TOut* __restrict__ o, const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hk, int Hv) {
-  // (ws and q are not __restrict__: that keeps the compiler from sinking the prefetch loads below the
-  // LDS barriers, whose asm memory clobber then pins them where they are issued)
+    const uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out, TOut* __restrict__ o,
+    const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hv) {
+  // (ws is not __restrict__: that keeps the compiler from sinking the prefetch loads below the LDS
+  // barriers, whose asm memory clobber then pins them where they are issued)
   __shared__ StateShared sh;
 
   // XCD-aware order: the DV/VB workgroups of one (sequence, head) are `pairs` ids apart, so with
@@ -532,11 +604,8 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 
   StateArgs a;
   a.ws = ws;
-  a.q = q;
-  a.Hk = Hk;
   a.Hv = Hv;
   a.h = h;
-  a.hk = h / (Hv / Hk);
   a.vb = vb;
   if (cu != nullptr) {
     a.bos = cu[seq];
@@ -576,11 +645,11 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
                  hipStream_t stream) {
   dim3 grid(nchunks, Hv);
   if (gate)
-    hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
+    hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
                        chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
   else
-    hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(64 * P1_WAVES), 0, stream, (const uint16_t*)q,
+    hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
                        chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
 }
@@ -632,7 +701,7 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
                               N, T, scale, qk_l2norm, ws, s);
   }
   dim3 grid2(N * Hv * (DV / VB));
-  hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, (const uint16_t*)q,
-                     initial_state, final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hk, Hv);
+  hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,
+                     (bf16*)o, cu_seqlens, N, n_chunks, T, Hv);
   return check_launch(fn);
 }
