@@ -29,6 +29,8 @@
 // D: row 4*(lane/16)+i, column lane%16) and v_mfma_f32_16x16x4_f32 (A[lane%16][lane/16], B[lane/16][lane%16])
 // for the fp32 block inverse. The contraction index of the [W'; Q'] S^T pass is taken in a permuted key order
 // (kappa below) so that two 16 x 16 D tiles of W'^T computed in phase 1 are directly one A fragment.
+#include <algorithm>
+
 #include "gdn_common.h"
 
 namespace zgdn {
@@ -156,9 +158,10 @@ struct Prep {
   float Ys[P1_WAVES][16][20];  // per-wave 16x16 scratch of the block inverse
   float Gs[CH];
   float Bs[CH];
+  float Rk[CH];  // per-token L2 factor of k (1 without the fused norm)
+  float Ai[CH];  // beta rk: row factor of A
+  float Pi[CH];  // s rq: row factor of P
   float Bk[CH];  // beta exp(G) rk
-  float Rq[CH];  // per-token L2 factors of q and k (1 without the fused norm)
-  float Rk[CH];
   float Fq[CH];  // s exp(G) rq
   float Fk[CH];  // exp(G_L - G) rk
 };
@@ -198,252 +201,310 @@ __device__ __forceinline__ void zero_upper_blocks(uint16_t* m, int ld) {
 // Contraction length over tokens for token tile tb of a lower-triangular left operand.
 __device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
 
+// Inputs of one chunk x head held in registers: the next item's are loaded while the current one is processed.
+struct PrepIn {
+  uint4 q0, q1, k0, k1, v0, v1;  // rows r0, r0 + 1 of this thread's row pair, 8 columns
+  float g, b;                    // last wave: token l's gate and beta
+};
+
+// Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
 template <typename TG, bool GATE>
 __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
-    int n_seqs, int T, int Hk, int Hv, float scale, int qk_l2norm, uint8_t* __restrict__ ws) {
+    int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, uint8_t* __restrict__ ws) {
   __shared__ Prep sm;
-  const int c = blockIdx.x, h = blockIdx.y;
-  const int hk = h / (Hv / Hk);
   const int tid = threadIdx.x, l = lane_id(), wave = tid >> 6;
-  const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
-  uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
+  const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // step 1: 32 row pairs x 16 column groups
+  const int r0 = 2 * p, r1 = 2 * p + 1;
 
-  // 1. rows of q, k, v -> LDS as row pairs (zeros past the chunk end): Q, K row-major, K^T and V^T.
-  {
-    const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // 32 row pairs x 16 column groups
-    const int r0 = 2 * p, r1 = 2 * p + 1;
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
-    if (r0 < cr.len) {
-      const size_t t = (size_t)(cr.t0 + r0);
-      q0 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
-      k0 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
-      v0 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
+  // The loads are unconditional (rows clamped into the chunk, masked when used) so the compiler can count
+  // them exactly: the wait for them at the next item then does not also wait for this item's stores.
+  auto load_in = [&](int item, PrepIn& x) {
+    const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
+    const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+    if (cr.len <= 0) return;  // nothing to read (the rows are masked to zero when used)
+    const size_t ta = (size_t)(cr.t0 + min(r0, cr.len - 1)), tb = (size_t)(cr.t0 + min(r1, cr.len - 1));
+    x.q0 = *reinterpret_cast<const uint4*>(q + (ta * Hk + hk) * DK + c8);
+    x.k0 = *reinterpret_cast<const uint4*>(k + (ta * Hk + hk) * DK + c8);
+    x.v0 = *reinterpret_cast<const uint4*>(v + (ta * Hv + h) * DV + c8);
+    x.q1 = *reinterpret_cast<const uint4*>(q + (tb * Hk + hk) * DK + c8);
+    x.k1 = *reinterpret_cast<const uint4*>(k + (tb * Hk + hk) * DK + c8);
+    x.v1 = *reinterpret_cast<const uint4*>(v + (tb * Hv + h) * DV + c8);
+    if (wave == P1_WAVES - 1) {
+      const size_t gh = (size_t)(cr.t0 + min(l, cr.len - 1)) * Hv + h;
+      x.g = io<TG>::load(g + gh);
+      x.b = io<TG>::load(beta + gh);
     }
-    if (r1 < cr.len) {
-      const size_t t = (size_t)(cr.t0 + r1);
-      q1 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
-      k1 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
-      v1 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
-    }
-    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r0][c8]) = q0;
-    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r1][c8]) = q1;
-    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r0][c8]) = k0;
-    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r1][c8]) = k1;
-    store_pair_t(&sm.KsT[0][0], LDC, c8, r0, k0, k1);
-    store_pair_t(&sm.VsT[0][0], LDC, c8, r0, v0, v1);
-  }
-  if (wave == P1_WAVES - 1) {
-    float gi = 0.f, bi = 0.f;
-    if (l < cr.len) {
-      const size_t gh = (size_t)(cr.t0 + l) * Hv + h;
-      gi = io<TG>::load(g + gh);
-      if constexpr (GATE) gi = -__expf(A_log[h]) * softplus(gi + dt_bias[h]);
-      bi = io<TG>::load(beta + gh);
-    }
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
-      const float o = __shfl_up(gi, d);
-      if (l >= d) gi += o;
-    }
-    sm.Gs[l] = gi;
-    sm.Bs[l] = bi;
-  }
-  __syncthreads();
+  };
 
-  // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127)
-  if (tid < 2 * CH) {
-    const int r = tid & (CH - 1);
-    const uint16_t* row = tid < CH ? &sm.u.a.Qs[r][0] : &sm.u.a.Ks[r][0];
-    float ss = 0.f;
+  int item = blockIdx.x;
+  PrepIn nx;
+  nx.q0 = nx.q1 = nx.k0 = nx.k1 = nx.v0 = nx.v1 = make_uint4(0, 0, 0, 0);
+  nx.g = nx.b = 0.f;
+  // the item loop with its first pass peeled: the loop is then entered, as at its back edge, with this
+  // item's stores issued after the prefetch, so the wait for the prefetch does not cover the stores
+  auto process = [&](int item) {
+    const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
+    const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+    uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
+    PrepIn in = nx;
+    {  // zero the rows past the chunk end
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      if (r0 >= cr.len) in.q0 = in.k0 = in.v0 = z;
+      if (r1 >= cr.len) in.q1 = in.k1 = in.v1 = z;
+      if (l >= cr.len) in.g = in.b = 0.f;
+    }
+
+    // 1. rows of q, k, v -> LDS (zeros past the chunk end): Q, K row-major, K^T and V^T; gate and G.
+    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r0][c8]) = in.q0;
+    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r1][c8]) = in.q1;
+    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r0][c8]) = in.k0;
+    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r1][c8]) = in.k1;
+    store_pair_t(&sm.KsT[0][0], LDC, c8, r0, in.k0, in.k1);
+    store_pair_t(&sm.VsT[0][0], LDC, c8, r0, in.v0, in.v1);
+    if (wave == P1_WAVES - 1) {
+      float gi = in.g;
+      if constexpr (GATE) gi = l < cr.len ? -__expf(A_log[h]) * softplus(gi + dt_bias[h]) : 0.f;
 #pragma unroll
-    for (int c8 = 0; c8 < DK; c8 += 8) {
-      const uint4 w = *reinterpret_cast<const uint4*>(row + c8);
-      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xffff0000u);
-        ss = fmaf(lo, lo, fmaf(hi, hi, ss));
+      for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
+        const float o = __shfl_up(gi, d);
+        if (l >= d) gi += o;
       }
-    }
-    const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-    const float gr = sm.Gs[r];
-    if (tid < CH) {
-      sm.Rq[r] = rf;
-      sm.Fq[r] = scale * __expf(gr) * rf;
-    } else {
-      sm.Rk[r] = rf;
-      sm.Fk[r] = __expf(sm.Gs[CH - 1] - gr) * rf;
-      sm.Bk[r] = sm.Bs[r] * __expf(gr) * rf;
-    }
-  }
-
-  // 2. K K^T and Q K^T on the 10 lower tiles each (20 tile jobs over 8 waves), kept in registers.
-  f32x4 acc[3];
-#pragma unroll
-  for (int m = 0; m < 3; ++m) {
-    const int job = wave + P1_WAVES * m;
-    acc[m] = zero4();
-    if (job < 20) {
-      int rb, cb;
-      lower_tile(job % 10, rb, cb);
-      const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
-      acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
-    }
-  }
-  __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
-#pragma unroll
-  for (int m = 0; m < 3; ++m) {
-    const int job = wave + P1_WAVES * m;
-    if (job < 20) {
-      int rb, cb;
-      lower_tile(job % 10, rb, cb);
-      const int j = cb * 16 + (l & 15);
-      const float gj = sm.Gs[j], rkj = sm.Rk[j];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int i = rb * 16 + 4 * (l >> 4) + i4;
-        const float e = __expf(sm.Gs[i] - gj) * rkj;
-        if (job < 10)
-          sm.u.b.As[i][j] = i > j ? sm.Bs[i] * sm.Rk[i] * e * acc[m][i4] : 0.f;
-        else
-          sm.Ps[i][j] = f32_to_bf16(i >= j ? scale * sm.Rq[i] * e * acc[m][i4] : 0.f);
-      }
-    }
-  }
-  zero_upper_blocks(&sm.Ps[0][0], LDC);
-  __syncthreads();
-
-  // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
-  if (wave == 0) {
-    const int b = l >> 4, col = l & 15, base = b * 16;
-    float t[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float4* arow = reinterpret_cast<const float4*>(&sm.u.b.As[base + r][base]);
-      float a[16];
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const float4 x = arow[q4];
-        a[4 * q4] = x.x; a[4 * q4 + 1] = x.y; a[4 * q4 + 2] = x.z; a[4 * q4 + 3] = x.w;
-      }
-      float s = (r == col) ? 1.f : 0.f;
-#pragma unroll
-      for (int jj = 0; jj < r; ++jj) s = fmaf(-a[jj], t[jj], s);
-      t[r] = s;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sm.u.b.Ts[base + r][base + col] = t[r];
-  }
-  __syncthreads();
-
-  // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA).
-  for (int bi = 1; bi < 4; ++bi) {
-    const int bj = wave;
-    if (bj < bi) {
-      f32x4 y = zero4();
-      for (int m = bj; m < bi; ++m)
-        y = mm16_f32(&sm.u.b.As[bi * 16][m * 16], LDF, &sm.u.b.Ts[m * 16][bj * 16], LDF, y);
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sm.Ys[wave][4 * (l >> 4) + i4][l & 15] = y[i4];
-      wave_sync_lds();
-      f32x4 z = mm16_f32(&sm.u.b.Ts[bi * 16][bi * 16], LDF, &sm.Ys[wave][0][0], 20, zero4());
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[bi * 16 + 4 * (l >> 4) + i4][bj * 16 + (l & 15)] = -z[i4];
+      sm.Gs[l] = gi;
+      sm.Bs[l] = in.b;
     }
     __syncthreads();
-  }
+    if (item + (int)gridDim.x < n_items) load_in(item + gridDim.x, nx);  // in flight until the next item
 
-  // 3c. the bf16 forms of T: TBF = diag(Fk) T diag(Bk), TBT = (T diag(Bk))^T, LB = (T - I) diag(beta).
-  for (int e = tid; e < CH * CH / 2; e += P1_THREADS) {
-    const int i = (2 * e) / CH, j = (2 * e) % CH;  // two adjacent columns j, j + 1 of row i
-    const float t0 = i >= j ? sm.u.b.Ts[i][j] : 0.f, t1 = i >= j + 1 ? sm.u.b.Ts[i][j + 1] : 0.f;
-    const float tb0 = t0 * sm.Bk[j], tb1 = t1 * sm.Bk[j + 1];
-    const float fk = sm.Fk[i];
-    *reinterpret_cast<uint32_t*>(&sm.TBF[i][j]) = pack_bf16x2(fk * tb0, fk * tb1);
-    *reinterpret_cast<uint32_t*>(&sm.LB[i][j]) = pack_bf16x2(i > j ? t0 * sm.Bs[j] : 0.f,
-                                                              i > j + 1 ? t1 * sm.Bs[j + 1] : 0.f);
-    sm.TBT[j][i] = f32_to_bf16(tb0);
-    sm.TBT[j + 1][i] = f32_to_bf16(tb1);
-  }
-  __syncthreads();
-
-  // 4. W' (as A fragments), Ub' (+ Ub^T in LDS), R = P T diag(Bk), and the K^T fragments.
-  {
-    uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
-    for (int job = wave; job < 16; job += P1_WAVES) {  // (token tile, k-step): W'^T = K^T TBF^T
-      const int tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-      const f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
-      const f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
-      gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
-    }
-    float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
-    for (int job = wave; job < 32; job += P1_WAVES) {  // (token tile, value block): Ub = beta V + LB V
-      const int tb = job >> 3, vb = job & 7;
-      const f32x4 u = tile_mm(&sm.LB[0][0], LDC, 16 * tb, &sm.VsT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
-      const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
-      const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
-      float ub[4];
-      ub[0] = fmaf(sm.Bs[i0], __uint_as_float(vv.x << 16), u[0]);
-      ub[1] = fmaf(sm.Bs[i0 + 1], __uint_as_float(vv.x & 0xffff0000u), u[1]);
-      ub[2] = fmaf(sm.Bs[i0 + 2], __uint_as_float(vv.y << 16), u[2]);
-      ub[3] = fmaf(sm.Bs[i0 + 3], __uint_as_float(vv.y & 0xffff0000u), u[3]);
-      gU[(vb * 4 + tb) * 64 + l] =
-          make_float4(sm.Fk[i0] * ub[0], sm.Fk[i0 + 1] * ub[1], sm.Fk[i0 + 2] * ub[2], sm.Fk[i0 + 3] * ub[3]);
-      *reinterpret_cast<uint2*>(&sm.u.c.UbT[n][i0]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
-    }
-    for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
-      int rb, cb;
-      lower_tile(job, rb, cb);
-      const f32x4 r = tile_mm(&sm.Ps[0][0], LDC, 16 * rb, &sm.TBT[0][0], LDC, 16 * cb, tri_kend(rb), zero4());
+    // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127)
+    if (tid < 2 * CH) {
+      const int r = tid & (CH - 1);
+      const uint16_t* row = tid < CH ? &sm.u.a.Qs[r][0] : &sm.u.a.Ks[r][0];
+      float ss = 0.f;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[16 * rb + 4 * (l >> 4) + i4][16 * cb + (l & 15)] = f32_to_bf16(r[i4]);
-    }
-    zero_upper_blocks(&sm.u.c.Rs[0][0], LDC);
-    uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
-    for (int e = tid; e < DK * CH / 8; e += P1_THREADS) {  // fragment f = 2 w + kk, lane ll
-      const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
-      gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[16 * w + (ll & 15)][32 * kk + 8 * (ll >> 4)]);
-    }
-  }
-  __syncthreads();
-
-  // 5. Q' = Fq q - R K (as A fragments) and Ob = P Ub (D tiles, bf16); G_L.
-  {
-    uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
-    for (int job = wave; job < 16; job += P1_WAVES) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
-      const int tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-      f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
-      f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
-      const int tok = 16 * tb + (l & 15);
-      uint2 c0 = make_uint2(0, 0), c1 = make_uint2(0, 0);
-      if (tok < cr.len) {  // raw q row (L2-resident since step 1)
-        const uint16_t* qrow = q + ((size_t)(cr.t0 + tok) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
-        c0 = *reinterpret_cast<const uint2*>(qrow);
-        c1 = *reinterpret_cast<const uint2*>(qrow + 16);
+      for (int cc = 0; cc < DK; cc += 8) {
+        const uint4 w = *reinterpret_cast<const uint4*>(row + cc);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xffff0000u);
+          ss = fmaf(lo, lo, fmaf(hi, hi, ss));
+        }
       }
-      const float fq = sm.Fq[tok];
-      d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
-      d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
-      d0[2] = fmaf(fq, __uint_as_float(c0.y << 16), -d0[2]);
-      d0[3] = fmaf(fq, __uint_as_float(c0.y & 0xffff0000u), -d0[3]);
-      d1[0] = fmaf(fq, __uint_as_float(c1.x << 16), -d1[0]);
-      d1[1] = fmaf(fq, __uint_as_float(c1.x & 0xffff0000u), -d1[1]);
-      d1[2] = fmaf(fq, __uint_as_float(c1.y << 16), -d1[2]);
-      d1[3] = fmaf(fq, __uint_as_float(c1.y & 0xffff0000u), -d1[3]);
-      gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+      const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+      const float gr = sm.Gs[r];
+      if (tid < CH) {
+        sm.Pi[r] = scale * rf;
+        sm.Fq[r] = scale * __expf(gr) * rf;
+      } else {
+        const float br = sm.Bs[r];
+        sm.Rk[r] = rf;
+        sm.Ai[r] = br * rf;
+        sm.Fk[r] = __expf(sm.Gs[CH - 1] - gr) * rf;
+        sm.Bk[r] = br * __expf(gr) * rf;
+      }
     }
-    uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
-    for (int job = wave; job < 32; job += P1_WAVES) {  // (token tile, value block): Ob = P Ub
-      const int tb = job >> 3, vb = job & 7;
-      const f32x4 y = tile_mm(&sm.Ps[0][0], LDC, 16 * tb, &sm.u.c.UbT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
-      gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+
+    // 2. K K^T and Q K^T on the 10 lower tiles each (20 tile jobs over 8 waves), kept in registers.
+    f32x4 acc[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const int job = wave + P1_WAVES * m;
+      acc[m] = zero4();
+      if (job < 20) {
+        int rb, cb;
+        lower_tile(job % 10, rb, cb);
+        const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
+        acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
+      }
     }
-    if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
-  }
+    __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
+    // A_ij = beta_i rk_i exp(G_i - G_j) rk_j k_i.k_j (i > j), P_ij = s rq_i exp(G_i - G_j) rk_j q_i.k_j (i >= j)
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const int job = wave + P1_WAVES * m;
+      if (job < 20) {
+        int rb, cb;
+        lower_tile(job % 10, rb, cb);
+        const int j = cb * 16 + (l & 15), i0 = rb * 16 + 4 * (l >> 4);
+        const float gj = sm.Gs[j], rkj = sm.Rk[j];
+        const float4 gi = *reinterpret_cast<const float4*>(&sm.Gs[i0]);
+        const float4 fi = *reinterpret_cast<const float4*>(job < 10 ? &sm.Ai[i0] : &sm.Pi[i0]);
+        const float gv[4] = {gi.x, gi.y, gi.z, gi.w}, fv[4] = {fi.x, fi.y, fi.z, fi.w};
+        float e[4];
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) e[i4] = fv[i4] * __expf(gv[i4] - gj) * rkj * acc[m][i4];
+        if (job < 10) {
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[i0 + i4][j] = i0 + i4 > j ? e[i4] : 0.f;
+        } else {
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) sm.Ps[i0 + i4][j] = f32_to_bf16(i0 + i4 >= j ? e[i4] : 0.f);
+        }
+      }
+    }
+    zero_upper_blocks(&sm.Ps[0][0], LDC);
+    __syncthreads();
+
+    // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
+    if (wave == 0) {
+      const int b = l >> 4, col = l & 15, base = b * 16;
+      float t[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float4* arow = reinterpret_cast<const float4*>(&sm.u.b.As[base + r][base]);
+        float a[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 x = arow[q4];
+          a[4 * q4] = x.x; a[4 * q4 + 1] = x.y; a[4 * q4 + 2] = x.z; a[4 * q4 + 3] = x.w;
+        }
+        float s = (r == col) ? 1.f : 0.f;
+#pragma unroll
+        for (int jj = 0; jj < r; ++jj) s = fmaf(-a[jj], t[jj], s);
+        t[r] = s;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sm.u.b.Ts[base + r][base + col] = t[r];
+    }
+    __syncthreads();
+
+    // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA).
+    for (int bi = 1; bi < 4; ++bi) {
+      const int bj = wave;
+      if (bj < bi) {
+        f32x4 y = zero4();
+        for (int m = bj; m < bi; ++m)
+          y = mm16_f32(&sm.u.b.As[bi * 16][m * 16], LDF, &sm.u.b.Ts[m * 16][bj * 16], LDF, y);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) sm.Ys[wave][4 * (l >> 4) + i4][l & 15] = y[i4];
+        wave_sync_lds();
+        f32x4 z = mm16_f32(&sm.u.b.Ts[bi * 16][bi * 16], LDF, &sm.Ys[wave][0][0], 20, zero4());
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[bi * 16 + 4 * (l >> 4) + i4][bj * 16 + (l & 15)] = -z[i4];
+      }
+      __syncthreads();
+    }
+
+    // 3c. the bf16 forms of T, in 2x2 blocks: TBF = diag(Fk) T diag(Bk), TBT = (T diag(Bk))^T,
+    // LB = (T - I) diag(beta). (The blocks above the diagonal of Ts are never written: masked here.)
+    for (int e = tid; e < (CH / 2) * (CH / 2); e += P1_THREADS) {
+      const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
+      const float2 ta = *reinterpret_cast<const float2*>(&sm.u.b.Ts[i][j]);
+      const float2 tc = *reinterpret_cast<const float2*>(&sm.u.b.Ts[i + 1][j]);
+      const float t00 = i >= j ? ta.x : 0.f, t01 = i > j ? ta.y : 0.f;
+      const float t10 = i + 1 >= j ? tc.x : 0.f, t11 = i >= j ? tc.y : 0.f;
+      const float2 bk = *reinterpret_cast<const float2*>(&sm.Bk[j]);
+      const float2 bs = *reinterpret_cast<const float2*>(&sm.Bs[j]);
+      const float2 fk = *reinterpret_cast<const float2*>(&sm.Fk[i]);
+      const float b00 = t00 * bk.x, b01 = t01 * bk.y, b10 = t10 * bk.x, b11 = t11 * bk.y;
+      *reinterpret_cast<uint32_t*>(&sm.TBF[i][j]) = pack_bf16x2(fk.x * b00, fk.x * b01);
+      *reinterpret_cast<uint32_t*>(&sm.TBF[i + 1][j]) = pack_bf16x2(fk.y * b10, fk.y * b11);
+      *reinterpret_cast<uint32_t*>(&sm.TBT[j][i]) = pack_bf16x2(b00, b10);
+      *reinterpret_cast<uint32_t*>(&sm.TBT[j + 1][i]) = pack_bf16x2(b01, b11);
+      *reinterpret_cast<uint32_t*>(&sm.LB[i][j]) = pack_bf16x2(i > j ? t00 * bs.x : 0.f, i > j + 1 ? t01 * bs.y : 0.f);
+      *reinterpret_cast<uint32_t*>(&sm.LB[i + 1][j]) =
+          pack_bf16x2(i + 1 > j ? t10 * bs.x : 0.f, i > j ? t11 * bs.y : 0.f);
+    }
+    __syncthreads();
+
+    // raw q of this wave's Q' jobs (step 5), loaded now so the latency is covered by step 4
+    uint2 cq[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3;
+      const int tok = 16 * tb + (l & 15);
+      cq[m][0] = cq[m][1] = make_uint2(0, 0);
+      if (cr.len > 0) {  // clamped row, masked in step 5
+        const uint16_t* qrow = q + ((size_t)(cr.t0 + min(tok, cr.len - 1)) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
+        cq[m][0] = *reinterpret_cast<const uint2*>(qrow);
+        cq[m][1] = *reinterpret_cast<const uint2*>(qrow + 16);
+      }
+    }
+
+    // 4. W' (as A fragments), Ub' (+ Ub^T in LDS), R = P T diag(Bk), and the K^T fragments.
+    {
+      uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {  // (token tile, k-step): W'^T = K^T TBF^T
+        const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
+        const f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
+        const f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
+        gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+      }
+      float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {  // (token tile, value block): Ub = beta V + LB V
+        const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
+        const f32x4 u = tile_mm(&sm.LB[0][0], LDC, 16 * tb, &sm.VsT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+        const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
+        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
+        const float4 bs = *reinterpret_cast<const float4*>(&sm.Bs[i0]);
+        const float4 fk = *reinterpret_cast<const float4*>(&sm.Fk[i0]);
+        float ub[4];
+        ub[0] = fmaf(bs.x, __uint_as_float(vv.x << 16), u[0]);
+        ub[1] = fmaf(bs.y, __uint_as_float(vv.x & 0xffff0000u), u[1]);
+        ub[2] = fmaf(bs.z, __uint_as_float(vv.y << 16), u[2]);
+        ub[3] = fmaf(bs.w, __uint_as_float(vv.y & 0xffff0000u), u[3]);
+        gU[(vb * 4 + tb) * 64 + l] = make_float4(fk.x * ub[0], fk.y * ub[1], fk.z * ub[2], fk.w * ub[3]);
+        *reinterpret_cast<uint2*>(&sm.u.c.UbT[n][i0]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
+      }
+      for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
+        int rb, cb;
+        lower_tile(job, rb, cb);
+        const f32x4 r = tile_mm(&sm.Ps[0][0], LDC, 16 * rb, &sm.TBT[0][0], LDC, 16 * cb, tri_kend(rb), zero4());
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[16 * rb + 4 * (l >> 4) + i4][16 * cb + (l & 15)] = f32_to_bf16(r[i4]);
+      }
+      zero_upper_blocks(&sm.u.c.Rs[0][0], LDC);
+      uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
+#pragma unroll
+      for (int m = 0; m < DK * CH / 8 / P1_THREADS; ++m) {  // fragment f = 2 w + kk, lane ll
+        const int e = tid + P1_THREADS * m;
+        const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
+        gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[16 * w + (ll & 15)][32 * kk + 8 * (ll >> 4)]);
+      }
+    }
+    __syncthreads();
+
+    // 5. Q' = Fq q - R K (as A fragments) and Ob = P Ub (D tiles, bf16); G_L.
+    {
+      uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
+        const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
+        f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
+        f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
+        const int tok = 16 * tb + (l & 15);
+        const float fq = tok < cr.len ? sm.Fq[tok] : 0.f;
+        const uint2 c0 = cq[m][0], c1 = cq[m][1];
+        d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
+        d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
+        d0[2] = fmaf(fq, __uint_as_float(c0.y << 16), -d0[2]);
+        d0[3] = fmaf(fq, __uint_as_float(c0.y & 0xffff0000u), -d0[3]);
+        d1[0] = fmaf(fq, __uint_as_float(c1.x << 16), -d1[0]);
+        d1[1] = fmaf(fq, __uint_as_float(c1.x & 0xffff0000u), -d1[1]);
+        d1[2] = fmaf(fq, __uint_as_float(c1.y << 16), -d1[2]);
+        d1[3] = fmaf(fq, __uint_as_float(c1.y & 0xffff0000u), -d1[3]);
+        gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+      }
+      uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {  // (token tile, value block): Ob = P Ub
+        const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
+        const f32x4 y = tile_mm(&sm.Ps[0][0], LDC, 16 * tb, &sm.u.c.UbT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+        gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+      }
+      if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
+    }
+    __syncthreads();  // the next item's rows overwrite Qs / Ks (aliasing Rs / UbT) and K^T, V^T
+  };
+  if (item >= n_items) return;
+  load_in(item, nx);
+  process(item);
+  for (item += gridDim.x; item < n_items; item += gridDim.x) process(item);
 }
 
 // ----------------------------------------------------------------------------------------------- phase 2
@@ -643,15 +704,20 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
                  const int32_t* chunk_idx, int n_seqs, int T, float scale, int qk_l2norm, uint8_t* ws,
                  hipStream_t stream) {
-  dim3 grid(nchunks, Hv);
+  // one resident workgroup per CU (the LDS footprint allows one), each looping over items
+  int dev = 0, n_cu = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    n_cu = 256;
+  const int n_items = nchunks * Hv;
+  dim3 grid(std::min(n_items, std::max(1, n_cu)));
   if (gate)
     hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
+                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, ws);
   else
     hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, T, Hk, Hv, scale, qk_l2norm, ws);
+                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, ws);
 }
 
 }  // namespace
