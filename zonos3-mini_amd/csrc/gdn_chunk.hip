@@ -42,7 +42,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int CH = 64;    // chunk length
 constexpr int DK = 128;   // key dim
 constexpr int DV = 128;   // value dim
-constexpr int VB = 16;    // value rows per phase-2 workgroup
+constexpr int VB = 16;    // value rows per phase-2 workgroup (DV / VB = 8 workgroups per sequence x head)
 constexpr int LDQ = DK + 8;  // padded LDS row (bf16) of a 128-wide matrix
 constexpr int LDC = CH + 8;  // padded LDS row (bf16) of a 64-wide matrix
 constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
@@ -654,11 +654,13 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   // barriers, whose asm memory clobber then pins them where they are issued)
   __shared__ StateShared sh;
 
-  // XCD-aware order: the DV/VB workgroups of one (sequence, head) are `pairs` ids apart, so with
-  // pairs % 8 == 0 they share an XCD and its L2 (they read the same chunk workspace).
+  // XCD-aware order (workgroups go round-robin over the 8 XCDs): ids are taken in groups of 64 = 8 pairs
+  // (sequence, head) x 8 value blocks, with id % 8 = pair % 8, so the 8 workgroups of one pair run on one
+  // XCD at the same time and share its L2 copy of the chunk workspace. The grid is padded to whole groups.
   const int pairs = n_seqs * Hv;
   const int id = blockIdx.x;
-  const int pair = id % pairs, vb = id / pairs;
+  const int pair = (id / 64) * 8 + (id % 8), vb = (id % 64) / 8;
+  if (pair >= pairs) return;
   const int seq = pair / Hv, h = pair % Hv;
   const int l = lane_id(), wave = threadIdx.x >> 6;
   const int ncol = 16 * wave + (l & 15);
@@ -766,7 +768,7 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
       launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
                               N, T, scale, qk_l2norm, ws, s);
   }
-  dim3 grid2(N * Hv * (DV / VB));
+  dim3 grid2(((N * Hv + 7) / 8) * 64);  // groups of 8 (sequence, head) pairs x DV / VB = 8 value blocks
   hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,
                      (bf16*)o, cu_seqlens, N, n_chunks, T, Hv);
   return check_launch(fn);
