@@ -133,29 +133,88 @@ __device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, cons
 
 constexpr int P1_WAVES = 8;
 constexpr int P1_THREADS = 64 * P1_WAVES;
+constexpr int P1_WGS_PER_CU = 2;
+constexpr int P1_WAVES_PER_SIMD = P1_WGS_PER_CU * P1_WAVES / 4;  // caps the registers per wave at 512 / 4
+
+// Phase-1 LDS matrices are unpadded and XOR-swizzled: 16-byte chunk c of row r is stored at chunk
+// c ^ swz(r), which keeps the 16-row fragment reads and the D-layout writes free of bank conflicts without
+// padding, so that two workgroups fit on a CU. 256-byte rows (CPR = 16 chunks per row) swizzle with r % 16,
+// 128-byte rows (CPR = 8) with (r / 2) % 8.
+template <int CPR>
+__device__ __forceinline__ int swz(int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); }
+// element offset of (row, column): 16-bit elements (8 per chunk) and 32-bit elements (4 per chunk)
+template <int CPR>
+__device__ __forceinline__ int at16(int r, int c) { return r * (CPR * 8) + (((c >> 3) ^ swz<CPR>(r)) << 3) + (c & 7); }
+template <int CPR>
+__device__ __forceinline__ int at32(int r, int c) { return r * (CPR * 4) + (((c >> 2) ^ swz<CPR>(r)) << 2) + (c & 3); }
+
+// Per-lane parts of the swizzled fragment addresses, formed once per item. A fragment's rows r0 .. r0 + 15
+// start at a multiple of 16, so the swizzle of row r0 + lane%16 depends on the lane only and a fragment
+// address is the row-tile base plus one of these offsets (in elements).
+struct SwLane {
+  int row8, row16;  // (lane % 16) * row length, 128-byte and 256-byte rows
+  int k8[2];        // chunk offsets of k-steps 0, 1 (32 columns each) in 128-byte rows
+  int k16[4];       // chunk offsets of k-steps 0..3 in 256-byte rows
+  __device__ __forceinline__ explicit SwLane(int l) {
+    const int m = l & 15, g = l >> 4;
+    row8 = m * 64;
+    row16 = m * 128;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) k8[kk] = ((4 * kk + g) ^ (m >> 1)) << 3;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) k16[kk] = ((4 * kk + g) ^ m) << 3;
+  }
+};
+
+// MFMA A / B fragment (rows r0 + lane%16, columns 32 kk + 8*(lane/16) .. +7) of a swizzled bf16 matrix.
+template <int CPR>
+__device__ __forceinline__ bf16x8 sfrag(const uint16_t* m, int r0, int kk, const SwLane& sw) {
+  const int off = CPR == 16 ? r0 * 128 + sw.row16 + sw.k16[kk] : r0 * 64 + sw.row8 + sw.k8[kk];
+  return *reinterpret_cast<const bf16x8*>(m + off);
+}
+
+// Tile (r0.., c0..) of A . B for swizzled A (row-major) and Bt (B transposed), contraction over [0, kend).
+template <int CPRA, int CPRB>
+__device__ __forceinline__ f32x4 stile(const uint16_t* A, int r0, const uint16_t* Bt, int c0, int kend,
+                                       const SwLane& sw, f32x4 acc) {
+#pragma unroll
+  for (int kk = 0; kk < (CPRA == 16 ? 4 : 2); ++kk)
+    if (32 * kk < kend) acc = mfma(sfrag<CPRA>(A, r0, kk, sw), sfrag<CPRB>(Bt, c0, kk, sw), acc);
+  return acc;
+}
+
+// 16x16x16 fp32 block product acc += A[ra.., ca..] . B[rb.., cb..] of swizzled 64x64 fp32 matrices.
+__device__ __forceinline__ f32x4 mm16_f32(const float* A, int ra, int ca, const float* B, int rb, int cb, int l,
+                                          f32x4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[at32<16>(ra + (l & 15), ca + 4 * s + (l >> 4))],
+                                                B[at32<16>(rb + 4 * s + (l >> 4), cb + (l & 15))], acc, 0, 0, 0);
+  return acc;
+}
 
 struct Prep {
+  // one 32 KiB region reused by phase: raw q, k rows -> A, T (fp32) -> the bf16 forms of T and R -> Ub^T
   union {
     struct {
-      uint16_t Qs[CH][LDQ];  // raw q, k rows (operands of K K^T, Q K^T)
-      uint16_t Ks[CH][LDQ];
+      uint16_t Qs[CH * DK];  // raw q, k rows, 256-byte rows (operands of K K^T, Q K^T)
+      uint16_t Ks[CH * DK];
     } a;
     struct {
-      float As[CH][LDF];  // strictly lower A (fp32)
-      float Ts[CH][LDF];  // T = (I + A)^-1 (fp32)
+      float As[CH * CH];  // strictly lower A (fp32, 256-byte rows); rows 0-15 above the diagonal blocks hold
+      float Ts[CH * CH];  // the block inverse's per-wave scratch.  T = (I + A)^-1 (fp32)
     } b;
     struct {
-      uint16_t Rs[CH][LDC];   // R = P T diag(beta exp(G) rk)  (bf16), so that P W = R K
-      uint16_t UbT[DV][LDC];  // Ub^T (bf16): B operand of Ob = P Ub
+      uint16_t TBF[CH * CH];  // diag(Fk) T diag(beta exp(G) rk)   (B operand of W'^T)
+      uint16_t TBT[CH * CH];  // (T diag(beta exp(G) rk))^T         (B operand of R)
+      uint16_t LB[CH * CH];   // (T - I) diag(beta)                 (A operand of Ub)
+      uint16_t Rs[CH * CH];   // R = P T diag(beta exp(G) rk), so that P W = R K (B operand of Q'^T)
     } c;
+    uint16_t UbT[DV * CH];  // Ub^T (B operand of Ob = P Ub), over TBF and TBT once W' and R are formed
   } u;
-  uint16_t KsT[DK][LDC];  // raw k^T: A operand of W'^T, Q'^T; source of the K^T fragments
-  uint16_t VsT[DV][LDC];  // v^T: B operand of Ub, and the exact diagonal term
-  uint16_t Ps[CH][LDC];   // P (bf16, zero above the diagonal blocks)
-  uint16_t TBF[CH][LDC];  // diag(Fk) T diag(beta exp(G) rk)   (B operand of W'^T)
-  uint16_t TBT[CH][LDC];  // (T diag(beta exp(G) rk))^T         (B operand of R)
-  uint16_t LB[CH][LDC];   // (T - I) diag(beta)                 (A operand of Ub)
-  float Ys[P1_WAVES][16][20];  // per-wave 16x16 scratch of the block inverse
+  uint16_t KsT[DK * CH];  // raw k^T: A operand of W'^T, Q'^T; source of the K^T fragments
+  uint16_t VsT[DV * CH];  // v^T: B operand of Ub, and the exact diagonal term
+  uint16_t Ps[CH * CH];   // P (bf16, zero above the diagonal blocks)
   float Gs[CH];
   float Bs[CH];
   float Rk[CH];  // per-token L2 factor of k (1 without the fused norm)
@@ -166,13 +225,13 @@ struct Prep {
   float Fk[CH];  // exp(G_L - G) rk
 };
 
-// Row-pair transposed store: dst[(c8 + i) * ld + r] <- (a[i], b[i]) as one 32-bit word (rows r, r + 1).
-__device__ __forceinline__ void store_pair_t(uint16_t* dst, int ld, int c8, int r, uint4 a, uint4 b) {
+// Row-pair transposed store into a swizzled [.][64] bf16 matrix: dst(c8 + i, r .. r + 1) <- (a[i], b[i]).
+__device__ __forceinline__ void store_pair_t(uint16_t* dst, int c8, int r, uint4 a, uint4 b) {
   const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint32_t*>(dst + (c8 + 2 * i) * ld + r) = (wa[i] & 0xffffu) | (wb[i] << 16);
-    *reinterpret_cast<uint32_t*>(dst + (c8 + 2 * i + 1) * ld + r) = (wa[i] >> 16) | (wb[i] & 0xffff0000u);
+    *reinterpret_cast<uint32_t*>(dst + at16<8>(c8 + 2 * i, r)) = (wa[i] & 0xffffu) | (wb[i] << 16);
+    *reinterpret_cast<uint32_t*>(dst + at16<8>(c8 + 2 * i + 1, r)) = (wa[i] >> 16) | (wb[i] & 0xffff0000u);
   }
 }
 
@@ -188,104 +247,93 @@ __device__ __forceinline__ void lower_tile(int t, int& rb, int& cb) {
   cb = t - rb * (rb + 1) / 2;
 }
 
-// Zero the 6 blocks above the diagonal of a 64x64 bf16 matrix with 16x16 blocks.
-__device__ __forceinline__ void zero_upper_blocks(uint16_t* m, int ld) {
+// Zero the 6 blocks above the diagonal of a swizzled 64x64 bf16 matrix with 16x16 blocks.
+__device__ __forceinline__ void zero_upper_blocks(uint16_t* m) {
   for (int e = threadIdx.x; e < 6 * 256; e += P1_THREADS) {
     const int t = e / 256, w = e % 256;
     const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
     const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    m[(rb * 16 + w / 16) * ld + cb * 16 + w % 16] = 0;
+    m[at16<8>(rb * 16 + w / 16, cb * 16 + w % 16)] = 0;
   }
 }
 
 // Contraction length over tokens for token tile tb of a lower-triangular left operand.
 __device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
 
-// Inputs of one chunk x head held in registers: the next item's are loaded while the current one is processed.
-struct PrepIn {
-  uint4 q0, q1, k0, k1, v0, v1;  // rows r0, r0 + 1 of this thread's row pair, 8 columns
-  float g, b;                    // last wave: token l's gate and beta
-};
-
 // Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
+// Two workgroups share a CU, so one's loads and barriers overlap the other's work.
 template <typename TG, bool GATE>
-__global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
+__global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
     int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, uint8_t* __restrict__ ws) {
   __shared__ Prep sm;
-  const int tid = threadIdx.x, l = lane_id(), wave = tid >> 6;
-  const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // step 1: 32 row pairs x 16 column groups
-  const int r0 = 2 * p, r1 = 2 * p + 1;
+  const int wave = threadIdx.x >> 6;
 
-  // The loads are unconditional (rows clamped into the chunk, masked when used) so the compiler can count
-  // them exactly: the wait for them at the next item then does not also wait for this item's stores.
-  auto load_in = [&](int item, PrepIn& x) {
-    const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
-    const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
-    if (cr.len <= 0) return;  // nothing to read (the rows are masked to zero when used)
-    const size_t ta = (size_t)(cr.t0 + min(r0, cr.len - 1)), tb = (size_t)(cr.t0 + min(r1, cr.len - 1));
-    x.q0 = *reinterpret_cast<const uint4*>(q + (ta * Hk + hk) * DK + c8);
-    x.k0 = *reinterpret_cast<const uint4*>(k + (ta * Hk + hk) * DK + c8);
-    x.v0 = *reinterpret_cast<const uint4*>(v + (ta * Hv + h) * DV + c8);
-    x.q1 = *reinterpret_cast<const uint4*>(q + (tb * Hk + hk) * DK + c8);
-    x.k1 = *reinterpret_cast<const uint4*>(k + (tb * Hk + hk) * DK + c8);
-    x.v1 = *reinterpret_cast<const uint4*>(v + (tb * Hv + h) * DV + c8);
-    if (wave == P1_WAVES - 1) {
-      const size_t gh = (size_t)(cr.t0 + min(l, cr.len - 1)) * Hv + h;
-      x.g = io<TG>::load(g + gh);
-      x.b = io<TG>::load(beta + gh);
-    }
-  };
-
-  int item = blockIdx.x;
-  PrepIn nx;
-  nx.q0 = nx.q1 = nx.k0 = nx.k1 = nx.v0 = nx.v1 = make_uint4(0, 0, 0, 0);
-  nx.g = nx.b = 0.f;
-  // the item loop with its first pass peeled: the loop is then entered, as at its back edge, with this
-  // item's stores issued after the prefetch, so the wait for the prefetch does not cover the stores
-  auto process = [&](int item) {
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    // thread indices made opaque per item: the swizzled LDS addresses derived from them are then formed
+    // where they are used instead of being hoisted out of the loop and kept live (or spilled) throughout
+    int tz = 0;
+    asm volatile("" : "+v"(tz));
+    const int tid = (int)threadIdx.x + tz, l = tid & 63;
+    const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // step 1: 32 row pairs x 16 column groups
+    const int r0 = 2 * p, r1 = 2 * p + 1;
+    const SwLane sw(l);
     const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
     const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
     uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
-    PrepIn in = nx;
-    {  // zero the rows past the chunk end
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      if (r0 >= cr.len) in.q0 = in.k0 = in.v0 = z;
-      if (r1 >= cr.len) in.q1 = in.k1 = in.v1 = z;
-      if (l >= cr.len) in.g = in.b = 0.f;
-    }
 
     // 1. rows of q, k, v -> LDS (zeros past the chunk end): Q, K row-major, K^T and V^T; gate and G.
-    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r0][c8]) = in.q0;
-    *reinterpret_cast<uint4*>(&sm.u.a.Qs[r1][c8]) = in.q1;
-    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r0][c8]) = in.k0;
-    *reinterpret_cast<uint4*>(&sm.u.a.Ks[r1][c8]) = in.k1;
-    store_pair_t(&sm.KsT[0][0], LDC, c8, r0, in.k0, in.k1);
-    store_pair_t(&sm.VsT[0][0], LDC, c8, r0, in.v0, in.v1);
+    {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
+      if (r0 < cr.len) {
+        const size_t t = (size_t)(cr.t0 + r0);
+        q0 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
+        k0 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
+        v0 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
+      }
+      if (r1 < cr.len) {
+        const size_t t = (size_t)(cr.t0 + r1);
+        q1 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
+        k1 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
+        v1 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
+      }
+      *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r0, c8)]) = q0;
+      *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r1, c8)]) = q1;
+      *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r0, c8)]) = k0;
+      *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r1, c8)]) = k1;
+      store_pair_t(sm.KsT, c8, r0, k0, k1);
+      store_pair_t(sm.VsT, c8, r0, v0, v1);
+    }
     if (wave == P1_WAVES - 1) {
-      float gi = in.g;
-      if constexpr (GATE) gi = l < cr.len ? -__expf(A_log[h]) * softplus(gi + dt_bias[h]) : 0.f;
+      float gi = 0.f, bi = 0.f;
+      if (l < cr.len) {
+        const size_t gh = (size_t)(cr.t0 + l) * Hv + h;
+        gi = io<TG>::load(g + gh);
+        if constexpr (GATE) gi = -__expf(A_log[h]) * softplus(gi + dt_bias[h]);
+        bi = io<TG>::load(beta + gh);
+      }
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
         const float o = __shfl_up(gi, d);
         if (l >= d) gi += o;
       }
       sm.Gs[l] = gi;
-      sm.Bs[l] = in.b;
+      sm.Bs[l] = bi;
     }
     __syncthreads();
-    if (item + (int)gridDim.x < n_items) load_in(item + gridDim.x, nx);  // in flight until the next item
 
-    // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127)
+    // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127); the sum of
+    // squares runs over the stored chunks in any order
     if (tid < 2 * CH) {
       const int r = tid & (CH - 1);
-      const uint16_t* row = tid < CH ? &sm.u.a.Qs[r][0] : &sm.u.a.Ks[r][0];
+      const uint16_t* row = (tid < CH ? sm.u.a.Qs : sm.u.a.Ks) + r * DK;
       float ss = 0.f;
 #pragma unroll
-      for (int cc = 0; cc < DK; cc += 8) {
-        const uint4 w = *reinterpret_cast<const uint4*>(row + cc);
+      for (int cc = 0; cc < DK; cc += 8) {  // chunk (cc / 8 + r) % 16: the rows' reads spread over the banks
+        const uint4 w = *reinterpret_cast<const uint4*>(row + ((cc + 8 * r) & (DK - 1)));
         const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -316,8 +364,7 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
       if (job < 20) {
         int rb, cb;
         lower_tile(job % 10, rb, cb);
-        const uint16_t* Am = job < 10 ? &sm.u.a.Ks[0][0] : &sm.u.a.Qs[0][0];
-        acc[m] = tile_mm(Am, LDQ, rb * 16, &sm.u.a.Ks[0][0], LDQ, cb * 16, DK, zero4());
+        acc[m] = stile<16, 16>(job < 10 ? sm.u.a.Ks : sm.u.a.Qs, rb * 16, sm.u.a.Ks, cb * 16, DK, sw, zero4());
       }
     }
     __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
@@ -338,14 +385,14 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
         for (int i4 = 0; i4 < 4; ++i4) e[i4] = fv[i4] * __expf(gv[i4] - gj) * rkj * acc[m][i4];
         if (job < 10) {
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[i0 + i4][j] = i0 + i4 > j ? e[i4] : 0.f;
+          for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[at32<16>(i0 + i4, j)] = i0 + i4 > j ? e[i4] : 0.f;
         } else {
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) sm.Ps[i0 + i4][j] = f32_to_bf16(i0 + i4 >= j ? e[i4] : 0.f);
+          for (int i4 = 0; i4 < 4; ++i4) sm.Ps[at16<8>(i0 + i4, j)] = f32_to_bf16(i0 + i4 >= j ? e[i4] : 0.f);
         }
       }
     }
-    zero_upper_blocks(&sm.Ps[0][0], LDC);
+    zero_upper_blocks(sm.Ps);
     __syncthreads();
 
     // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
@@ -354,59 +401,79 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
       float t[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float4* arow = reinterpret_cast<const float4*>(&sm.u.b.As[base + r][base]);
         float a[16];
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 x = arow[q4];
+          const float4 x = *reinterpret_cast<const float4*>(&sm.u.b.As[at32<16>(base + r, base + 4 * q4)]);
           a[4 * q4] = x.x; a[4 * q4 + 1] = x.y; a[4 * q4 + 2] = x.z; a[4 * q4 + 3] = x.w;
         }
-        float s = (r == col) ? 1.f : 0.f;
+        // two interleaved partial sums keep the dependent chain short
+        float s0 = (r == col) ? 1.f : 0.f, s1 = 0.f;
 #pragma unroll
-        for (int jj = 0; jj < r; ++jj) s = fmaf(-a[jj], t[jj], s);
-        t[r] = s;
+        for (int jj = 0; jj + 1 < r; jj += 2) {
+          s0 = fmaf(-a[jj], t[jj], s0);
+          s1 = fmaf(-a[jj + 1], t[jj + 1], s1);
+        }
+        if (r & 1) s0 = fmaf(-a[r - 1], t[r - 1], s0);
+        t[r] = s0 + s1;
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sm.u.b.Ts[base + r][base + col] = t[r];
+      for (int r = 0; r < 16; ++r) sm.u.b.Ts[at32<16>(base + r, base + col)] = t[r];
     }
     __syncthreads();
 
-    // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA).
+    // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA);
+    // wave w's scratch Y is the (unused) block (0, w + 1) of As
     for (int bi = 1; bi < 4; ++bi) {
       const int bj = wave;
       if (bj < bi) {
         f32x4 y = zero4();
-        for (int m = bj; m < bi; ++m)
-          y = mm16_f32(&sm.u.b.As[bi * 16][m * 16], LDF, &sm.u.b.Ts[m * 16][bj * 16], LDF, y);
+        for (int m = bj; m < bi; ++m) y = mm16_f32(sm.u.b.As, bi * 16, m * 16, sm.u.b.Ts, m * 16, bj * 16, l, y);
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.Ys[wave][4 * (l >> 4) + i4][l & 15] = y[i4];
+        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[at32<16>(4 * (l >> 4) + i4, 16 * (wave + 1) + (l & 15))] = y[i4];
         wave_sync_lds();
-        f32x4 z = mm16_f32(&sm.u.b.Ts[bi * 16][bi * 16], LDF, &sm.Ys[wave][0][0], 20, zero4());
+        f32x4 z = mm16_f32(sm.u.b.Ts, bi * 16, bi * 16, sm.u.b.As, 0, 16 * (wave + 1), l, zero4());
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[bi * 16 + 4 * (l >> 4) + i4][bj * 16 + (l & 15)] = -z[i4];
+        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[at32<16>(bi * 16 + 4 * (l >> 4) + i4, bj * 16 + (l & 15))] = -z[i4];
       }
       __syncthreads();
     }
 
-    // 3c. the bf16 forms of T, in 2x2 blocks: TBF = diag(Fk) T diag(Bk), TBT = (T diag(Bk))^T,
-    // LB = (T - I) diag(beta). (The blocks above the diagonal of Ts are never written: masked here.)
-    for (int e = tid; e < (CH / 2) * (CH / 2); e += P1_THREADS) {
-      const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
-      const float2 ta = *reinterpret_cast<const float2*>(&sm.u.b.Ts[i][j]);
-      const float2 tc = *reinterpret_cast<const float2*>(&sm.u.b.Ts[i + 1][j]);
-      const float t00 = i >= j ? ta.x : 0.f, t01 = i > j ? ta.y : 0.f;
-      const float t10 = i + 1 >= j ? tc.x : 0.f, t11 = i >= j ? tc.y : 0.f;
-      const float2 bk = *reinterpret_cast<const float2*>(&sm.Bk[j]);
-      const float2 bs = *reinterpret_cast<const float2*>(&sm.Bs[j]);
-      const float2 fk = *reinterpret_cast<const float2*>(&sm.Fk[i]);
-      const float b00 = t00 * bk.x, b01 = t01 * bk.y, b10 = t10 * bk.x, b11 = t11 * bk.y;
-      *reinterpret_cast<uint32_t*>(&sm.TBF[i][j]) = pack_bf16x2(fk.x * b00, fk.x * b01);
-      *reinterpret_cast<uint32_t*>(&sm.TBF[i + 1][j]) = pack_bf16x2(fk.y * b10, fk.y * b11);
-      *reinterpret_cast<uint32_t*>(&sm.TBT[j][i]) = pack_bf16x2(b00, b10);
-      *reinterpret_cast<uint32_t*>(&sm.TBT[j + 1][i]) = pack_bf16x2(b01, b11);
-      *reinterpret_cast<uint32_t*>(&sm.LB[i][j]) = pack_bf16x2(i > j ? t00 * bs.x : 0.f, i > j + 1 ? t01 * bs.y : 0.f);
-      *reinterpret_cast<uint32_t*>(&sm.LB[i + 1][j]) =
-          pack_bf16x2(i + 1 > j ? t10 * bs.x : 0.f, i > j ? t11 * bs.y : 0.f);
+    // 3c. the bf16 forms of T, in 2x2 blocks (through registers: they overwrite A and T): TBF = diag(Fk) T
+    // diag(Bk), TBT = (T diag(Bk))^T, LB = (T - I) diag(beta). (T above the diagonal blocks is masked.)
+    {
+      uint32_t wf[2][2], wt[2][2], wl[2][2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int e = tid + P1_THREADS * m;
+        const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
+        const float2 ta = *reinterpret_cast<const float2*>(&sm.u.b.Ts[at32<16>(i, j)]);
+        const float2 tc = *reinterpret_cast<const float2*>(&sm.u.b.Ts[at32<16>(i + 1, j)]);
+        const float t00 = i >= j ? ta.x : 0.f, t01 = i > j ? ta.y : 0.f;
+        const float t10 = i + 1 >= j ? tc.x : 0.f, t11 = i >= j ? tc.y : 0.f;
+        const float2 bk = *reinterpret_cast<const float2*>(&sm.Bk[j]);
+        const float2 bs = *reinterpret_cast<const float2*>(&sm.Bs[j]);
+        const float2 fk = *reinterpret_cast<const float2*>(&sm.Fk[i]);
+        const float b00 = t00 * bk.x, b01 = t01 * bk.y, b10 = t10 * bk.x, b11 = t11 * bk.y;
+        wf[m][0] = pack_bf16x2(fk.x * b00, fk.x * b01);
+        wf[m][1] = pack_bf16x2(fk.y * b10, fk.y * b11);
+        wt[m][0] = pack_bf16x2(b00, b10);
+        wt[m][1] = pack_bf16x2(b01, b11);
+        wl[m][0] = pack_bf16x2(i > j ? t00 * bs.x : 0.f, i > j + 1 ? t01 * bs.y : 0.f);
+        wl[m][1] = pack_bf16x2(i + 1 > j ? t10 * bs.x : 0.f, i > j ? t11 * bs.y : 0.f);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int e = tid + P1_THREADS * m;
+        const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
+        *reinterpret_cast<uint32_t*>(&sm.u.c.TBF[at16<8>(i, j)]) = wf[m][0];
+        *reinterpret_cast<uint32_t*>(&sm.u.c.TBF[at16<8>(i + 1, j)]) = wf[m][1];
+        *reinterpret_cast<uint32_t*>(&sm.u.c.TBT[at16<8>(j, i)]) = wt[m][0];
+        *reinterpret_cast<uint32_t*>(&sm.u.c.TBT[at16<8>(j + 1, i)]) = wt[m][1];
+        *reinterpret_cast<uint32_t*>(&sm.u.c.LB[at16<8>(i, j)]) = wl[m][0];
+        *reinterpret_cast<uint32_t*>(&sm.u.c.LB[at16<8>(i + 1, j)]) = wl[m][1];
+      }
     }
     __syncthreads();
 
@@ -417,30 +484,50 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
       const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3;
       const int tok = 16 * tb + (l & 15);
       cq[m][0] = cq[m][1] = make_uint2(0, 0);
-      if (cr.len > 0) {  // clamped row, masked in step 5
-        const uint16_t* qrow = q + ((size_t)(cr.t0 + min(tok, cr.len - 1)) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
+      if (tok < cr.len) {
+        const uint16_t* qrow = q + ((size_t)(cr.t0 + tok) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
         cq[m][0] = *reinterpret_cast<const uint2*>(qrow);
         cq[m][1] = *reinterpret_cast<const uint2*>(qrow + 16);
       }
     }
 
-    // 4. W' (as A fragments), Ub' (+ Ub^T in LDS), R = P T diag(Bk), and the K^T fragments.
+    // 4a. W' (as A fragments), R = P T diag(Bk), and the K^T fragments.
     {
       uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
 #pragma unroll
       for (int m = 0; m < 2; ++m) {  // (token tile, k-step): W'^T = K^T TBF^T
         const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        const f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
-        const f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.TBF[0][0], LDC, 16 * tb, kend, zero4());
+        const f32x4 d0 = stile<8, 8>(sm.KsT, 32 * kq, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
+        const f32x4 d1 = stile<8, 8>(sm.KsT, 32 * kq + 16, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
         gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
       }
+      for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
+        int rb, cb;
+        lower_tile(job, rb, cb);
+        const f32x4 r = stile<8, 8>(sm.Ps, 16 * rb, sm.u.c.TBT, 16 * cb, tri_kend(rb), sw, zero4());
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[at16<8>(16 * rb + 4 * (l >> 4) + i4, 16 * cb + (l & 15))] = f32_to_bf16(r[i4]);
+      }
+      zero_upper_blocks(sm.u.c.Rs);
+      uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
+#pragma unroll
+      for (int m = 0; m < DK * CH / 8 / P1_THREADS; ++m) {  // fragment f = 2 w + kk, lane ll
+        const int e = tid + P1_THREADS * m;
+        const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
+        gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[at16<8>(16 * w + (ll & 15), 32 * kk + 8 * (ll >> 4))]);
+      }
+    }
+    __syncthreads();  // Ub^T overwrites TBF, TBT
+
+    // 4b. Ub = beta V + LB V: Ub' = Fk Ub (D tiles, fp32) to the workspace, Ub^T (bf16) to LDS.
+    {
       float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {  // (token tile, value block): Ub = beta V + LB V
+      for (int m = 0; m < 4; ++m) {  // (token tile, value block)
         const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
-        const f32x4 u = tile_mm(&sm.LB[0][0], LDC, 16 * tb, &sm.VsT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+        const f32x4 u = stile<8, 8>(sm.u.c.LB, 16 * tb, sm.VsT, 16 * vb, tri_kend(tb), sw, zero4());
         const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
-        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[n][i0]);
+        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[at16<8>(n, i0)]);
         const float4 bs = *reinterpret_cast<const float4*>(&sm.Bs[i0]);
         const float4 fk = *reinterpret_cast<const float4*>(&sm.Fk[i0]);
         float ub[4];
@@ -449,22 +536,7 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
         ub[2] = fmaf(bs.z, __uint_as_float(vv.y << 16), u[2]);
         ub[3] = fmaf(bs.w, __uint_as_float(vv.y & 0xffff0000u), u[3]);
         gU[(vb * 4 + tb) * 64 + l] = make_float4(fk.x * ub[0], fk.y * ub[1], fk.z * ub[2], fk.w * ub[3]);
-        *reinterpret_cast<uint2*>(&sm.u.c.UbT[n][i0]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
-      }
-      for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
-        int rb, cb;
-        lower_tile(job, rb, cb);
-        const f32x4 r = tile_mm(&sm.Ps[0][0], LDC, 16 * rb, &sm.TBT[0][0], LDC, 16 * cb, tri_kend(rb), zero4());
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[16 * rb + 4 * (l >> 4) + i4][16 * cb + (l & 15)] = f32_to_bf16(r[i4]);
-      }
-      zero_upper_blocks(&sm.u.c.Rs[0][0], LDC);
-      uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
-#pragma unroll
-      for (int m = 0; m < DK * CH / 8 / P1_THREADS; ++m) {  // fragment f = 2 w + kk, lane ll
-        const int e = tid + P1_THREADS * m;
-        const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
-        gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[16 * w + (ll & 15)][32 * kk + 8 * (ll >> 4)]);
+        *reinterpret_cast<uint2*>(&sm.u.UbT[at16<8>(n, i0)]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
       }
     }
     __syncthreads();
@@ -475,10 +547,9 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
 #pragma unroll
       for (int m = 0; m < 2; ++m) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
         const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        f32x4 d0 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
-        f32x4 d1 = tile_mm(&sm.KsT[0][0], LDC, 32 * kq + 16, &sm.u.c.Rs[0][0], LDC, 16 * tb, kend, zero4());
-        const int tok = 16 * tb + (l & 15);
-        const float fq = tok < cr.len ? sm.Fq[tok] : 0.f;
+        f32x4 d0 = stile<8, 8>(sm.KsT, 32 * kq, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
+        f32x4 d1 = stile<8, 8>(sm.KsT, 32 * kq + 16, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
+        const float fq = sm.Fq[16 * tb + (l & 15)];
         const uint2 c0 = cq[m][0], c1 = cq[m][1];
         d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
         d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
@@ -494,17 +565,13 @@ __global__ __launch_bounds__(P1_THREADS) void chunk_prep_kernel(
 #pragma unroll
       for (int m = 0; m < 4; ++m) {  // (token tile, value block): Ob = P Ub
         const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
-        const f32x4 y = tile_mm(&sm.Ps[0][0], LDC, 16 * tb, &sm.u.c.UbT[0][0], LDC, 16 * vb, tri_kend(tb), zero4());
+        const f32x4 y = stile<8, 8>(sm.Ps, 16 * tb, sm.u.UbT, 16 * vb, tri_kend(tb), sw, zero4());
         gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
       }
       if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
     }
-    __syncthreads();  // the next item's rows overwrite Qs / Ks (aliasing Rs / UbT) and K^T, V^T
-  };
-  if (item >= n_items) return;
-  load_in(item, nx);
-  process(item);
-  for (item += gridDim.x; item < n_items; item += gridDim.x) process(item);
+    __syncthreads();  // the next item's rows overwrite Qs / Ks (aliasing Rs / Ub^T) and K^T, V^T
+  }
 }
 
 // ----------------------------------------------------------------------------------------------- phase 2
@@ -706,12 +773,12 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
                  const int32_t* chunk_idx, int n_seqs, int T, float scale, int qk_l2norm, uint8_t* ws,
                  hipStream_t stream) {
-  // one resident workgroup per CU (the LDS footprint allows one), each looping over items
+  // P1_WGS_PER_CU resident workgroups per CU (what the LDS footprint allows), each looping over items
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     n_cu = 256;
   const int n_items = nchunks * Hv;
-  dim3 grid(std::min(n_items, std::max(1, n_cu)));
+  dim3 grid(std::min(n_items, P1_WGS_PER_CU * std::max(1, n_cu)));
   if (gate)
     hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
