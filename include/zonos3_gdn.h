@@ -54,7 +54,7 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
 
 /*
  * Bytes of workspace zgdn_chunk_fwd needs for n_chunks 64-token chunks (over all sequences) and Hv value
- * heads (74,256 bytes per chunk and head).
+ * heads (98,560 bytes per chunk and head).
  */
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
 
