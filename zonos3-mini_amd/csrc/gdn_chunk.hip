@@ -652,9 +652,6 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     f32x4 x = zero4();
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk), x);
-    fetch2(wn, nxt);
-    fetch3(wn, nxt);
-    asm volatile("" ::: "memory");  // keeps the loads ahead of the output stores and the barrier
     if constexpr (URole) {
       // U' = Ub' - W' S^T as hi + lo bf16
       const float ub[4] = {__uint_as_float(cur.X.x), __uint_as_float(cur.X.y), __uint_as_float(cur.X.z),
@@ -679,6 +676,8 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
           io<TOut>::store(o + ((size_t)(a.bos + ci * CH + t) * a.Hv + a.h) * DV + a.vb * VB + j, ob[i4] + x[i4]);
       }
     }
+    fetch2(wn, nxt);
+    fetch3(wn, nxt);
     lds_barrier();
 
     // S <- exp(G_L) S + U'^T K for this wave's 16 columns
