@@ -40,8 +40,8 @@ BF16_PEAK_TFLOPS = 2500.0
 DECODE = dict(B=64, H=16, K=128, V=128)
 DECODE_BYTES_PER_TOKEN_HEAD = 2 * 128 * 128 * 4 + 2 * (128 + 128) * 2 + 2 * 4  # 132,104
 # HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the same
-# counter's reading of a plain 64 MiB copy (FETCH_SIZE x 1.9993, WRITE_SIZE x 1.0): 68,259 + 65,792 KiB
-TRAFFIC_DECODE = 137_268_224
+# counter's reading of a plain 64 MiB copy (FETCH_SIZE x 1.9993, WRITE_SIZE x 1.0): 67,042 + 65,795 KiB
+TRAFFIC_DECODE = 136_025_161
 
 
 def _args():
@@ -359,7 +359,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": TRAFFIC_DECODE,
-            "kernel": "recurrent_kernel<bf16,bf16,float,128,1,8>",
+            "kernel": "step_kernel<bf16,bf16,float,128,LEAN=true,GPT=4>",
             "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
             "algorithmic_bytes": dec["bytes_per_launch"],
         },

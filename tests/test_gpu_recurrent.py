@@ -121,3 +121,62 @@ def test_no_final_state_and_no_initial_state(gdn, cuda):
     assert s is None
     o_ref, _ = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
     assert rel_err(o.cpu(), o_ref) < 1e-4
+
+
+@pytest.mark.parametrize("case", ["fp32_k64_v40", "bf16_gva_bf16_gates", "gate_l2norm", "no_states", "b256",
+                                  "k64_tiled", "fp32_tiled"])
+def test_single_token_step(gdn, cuda, case):
+    """T = 1 without cu_seqlens runs the persistent single-token kernel: every input variant it takes (the
+    general form), small batches (one row group per item), and batches that take the tiled form (four row
+    groups sharing one q/k load), including one where each wave walks many tiles (B=256, H=16)."""
+    announce(f"single-token step {case}")
+    B, hk, hv, K, V, dtype, gb = 5, 2, 2, 128, 128, torch.bfloat16, torch.float32
+    if case == "fp32_k64_v40":
+        B, hk, hv, K, V, dtype = 3, 1, 1, 64, 40, torch.float32
+    elif case == "bf16_gva_bf16_gates":
+        B, hk, hv, gb = 7, 2, 8, torch.bfloat16
+    elif case == "b256":
+        B, hk, hv = 256, 16, 16
+    elif case == "k64_tiled":
+        B, hk, hv, K, V = 128, 8, 16, 64, 64
+    elif case == "fp32_tiled":
+        B, hk, hv, dtype = 64, 16, 16, torch.float32
+    d = O.make_inputs(B, 1, hk, hv, K, V, seed=1010, dtype=dtype, state_std=0.02)
+    if case == "gate_l2norm":
+        gen = torch.Generator().manual_seed(1011)
+        q = (2 * torch.randn(B, 1, hk, K, generator=gen)).to(dtype)
+        k = (2 * torch.randn(B, 1, hk, K, generator=gen)).to(dtype)
+        a = torch.randn(B, 1, hv, generator=gen)
+        A_log, dt_bias = 0.3 * torch.randn(hv, generator=gen), 0.3 * torch.randn(hv, generator=gen)
+        o, s = gdn.recurrent_fwd(q.to(cuda), k.to(cuda), d["v"].to(cuda), a.to(cuda), d["beta"].to(cuda),
+                                 initial_state=d["s0"].to(cuda), A_log=A_log.to(cuda), dt_bias=dt_bias.to(cuda),
+                                 use_qk_l2norm=True)
+        torch.cuda.synchronize()
+        g_log = -A_log.exp() * torch.nn.functional.softplus(a + dt_bias)
+        o_ref, s_ref = O.gated_delta_recurrence(O.l2norm(q), O.l2norm(k), d["v"], g_log, d["beta"], None, d["s0"])
+        o, s = o.cpu(), s.cpu()
+    elif case == "no_states":
+        q, k, v, g, b = (d[n].to(cuda) for n in ("q", "k", "v", "g", "beta"))
+        o, s = gdn.recurrent_fwd(q, k, v, g, b, output_final_state=False)
+        torch.cuda.synchronize()
+        assert s is None
+        o_ref, _ = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+        assert max_abs(o.cpu(), o_ref) < 2e-2
+        return
+    else:
+        o, s = _run(gdn, cuda, d, gb_dtype=gb, inplace=case == "b256")
+        o_ref, s_ref = _oracle(d, gb_dtype=gb)
+    _check(o, s, o_ref, s_ref, bf16=dtype == torch.bfloat16)
+    assert rel_err(s, s_ref) < 1e-5  # the state update is plain fp32 arithmetic
+
+
+def test_single_token_step_matches_token_loop_kernel(gdn, cuda):
+    """The same single-token batch through the persistent step kernel (B streams, T=1) and through the
+    token-loop kernel (packed as B one-token sequences): the same fp32 arithmetic, so equal to rounding."""
+    announce("single-token step vs token-loop kernel B=64 H=16")
+    d = O.make_inputs(64, 1, 8, 16, 128, 128, seed=1012, dtype=torch.bfloat16, state_std=0.02)
+    o1, s1 = _run(gdn, cuda, d)
+    d1 = {n: d[n] if n == "s0" else d[n].reshape(1, 64, *d[n].shape[2:]) for n in d}
+    o2, s2 = _run(gdn, cuda, d1, cu=list(range(65)))
+    assert rel_err(s1, s2) < 1e-6
+    assert rel_err(o1.reshape(o2.shape).float(), o2.float()) < 4e-3  # at most one bf16 rounding step apart

@@ -13,6 +13,8 @@
 //   delta = beta (v_j - alpha pk)
 //   S <- alpha S + delta k
 //   o_j = scale (alpha pq + delta (k.q))            (== S_new . q scale)
+#include <algorithm>
+
 #include "gdn_common.h"
 
 namespace zgdn {
@@ -143,6 +145,172 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------ single-token step (T == 1)
+//
+// One token per stream is one pass over the state, so the step is a stream of state rows with no reuse: the
+// kernel is persistent and software-pipelined. Work is split into tiles of GPT row groups (RPP rows each, one
+// row per LPR lanes, the register layout above) of one (stream, head), so a tile's q/k row, g and beta are
+// loaded once for GPT groups. Each wave walks tiles gridDim.x * STEP_NWAVES apart and issues the next tile's
+// loads (state rows, q/k row, v, g, beta) before it updates and stores the current tile, so a tile's reads
+// are always in flight while the wave computes and writes. Loads keep the raw input words and convert when
+// used, so issuing them never waits for data. The prefetch after a wave's last tile is clamped to the last
+// tile (an unused read) so that every iteration waits on the same, exact count of outstanding loads. The LEAN
+// form is the plain decode step (state read and written, g the log decay, q/k as given, V a multiple of the
+// tile's rows): its loads are all unconditional, so the compiler's wait counts stay exact; the other form
+// takes every option of the entry point.
+
+template <typename T>
+struct raw4;  // four consecutive inputs as loaded, and as floats
+template <>
+struct raw4<float> {
+  using type = float4;
+  __device__ __forceinline__ static type load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ static void unpack(type w, float* f) { f[0] = w.x; f[1] = w.y; f[2] = w.z; f[3] = w.w; }
+};
+template <>
+struct raw4<bf16> {
+  using type = uint2;
+  __device__ __forceinline__ static type load(const bf16* p) { return *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ static void unpack(type w, float* f) {
+    f[0] = __uint_as_float(w.x << 16); f[1] = __uint_as_float(w.x & 0xffff0000u);
+    f[2] = __uint_as_float(w.y << 16); f[3] = __uint_as_float(w.y & 0xffff0000u);
+  }
+};
+__device__ __forceinline__ float as_f32(float x) { return x; }
+__device__ __forceinline__ float as_f32(bf16 x) { return bf16_to_f32(x.bits); }
+
+template <typename TIn, typename TG, int GPT>
+struct StepTile {
+  float4 s[GPT][2];                                    // the lane's 8 state entries of its row in each group
+  typename raw4<TIn>::type ka, kb, qa, qb;             // the lane's 8 entries of k and q
+  TIn vj[GPT];
+  TG g, beta;
+  float a_log, dt_bias;
+};
+
+constexpr int STEP_NWAVES = 4;
+
+template <typename TIn, typename TOut, typename TG, int K, bool LEAN, int GPT>
+__global__ __launch_bounds__(64 * STEP_NWAVES) void step_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TG* __restrict__ g,
+    const TG* __restrict__ beta, const float* __restrict__ A_log, const float* __restrict__ dt_bias, int qk_l2norm,
+    const float* s_in, float* s_out, TOut* __restrict__ o, int n_tiles, int Hk, int Hv, int V, float scale) {
+  constexpr int LPR = K / 8, RPP = 64 / LPR, ROWS = RPP * GPT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, rsub = lane / LPR;
+  const int c0 = sub * 4, c1 = K / 2 + sub * 4;
+  const int tph = (V + ROWS - 1) / ROWS;  // tiles per (stream, head)
+  using Tile = StepTile<TIn, TG, GPT>;
+
+  auto load = [&](int ti, Tile& x) {
+    const int nh = ti / tph;  // stream * Hv + head: also the token row of g, beta, v
+    const int n = nh / Hv, h = nh - n * Hv, hk = h / (Hv / Hk);
+    const int row0 = (ti - nh * tph) * ROWS + rsub;
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      int row = row0 + j * RPP;
+      if constexpr (!LEAN) row = min(row, V - 1);  // clamped: no divergent load
+      if (LEAN || s_in != nullptr) {
+        const float* src = s_in + ((size_t)nh * V + row) * K;
+        x.s[j][0] = *reinterpret_cast<const float4*>(src + c0);
+        x.s[j][1] = *reinterpret_cast<const float4*>(src + c1);
+      } else {
+        x.s[j][0] = x.s[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    const size_t qk = ((size_t)n * Hk + hk) * K;
+    x.ka = raw4<TIn>::load(k + qk + c0);
+    x.kb = raw4<TIn>::load(k + qk + c1);
+    x.qa = raw4<TIn>::load(q + qk + c0);
+    x.qb = raw4<TIn>::load(q + qk + c1);
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      int row = row0 + j * RPP;
+      if constexpr (!LEAN) row = min(row, V - 1);
+      x.vj[j] = v[(size_t)nh * V + row];
+    }
+    x.g = g[nh];
+    x.beta = beta[nh];
+    if (!LEAN && A_log != nullptr) {
+      x.a_log = A_log[h];
+      x.dt_bias = dt_bias[h];
+    }
+  };
+
+  auto process = [&](int ti, const Tile& x) {
+    const int nh = ti / tph, row0 = (ti - nh * tph) * ROWS + rsub;
+    float kk[8], qq[8];
+    raw4<TIn>::unpack(x.ka, kk);
+    raw4<TIn>::unpack(x.kb, kk + 4);
+    raw4<TIn>::unpack(x.qa, qq);
+    raw4<TIn>::unpack(x.qb, qq + 4);
+    if (!LEAN && qk_l2norm) {  // x * rsqrt(sum x^2 + 1e-6) in fp32 (lm.py:570-571)
+      float nk = 0.f, nq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        nk = fmaf(kk[i], kk[i], nk);
+        nq = fmaf(qq[i], qq[i], nq);
+      }
+      const float rk = rsqrtf(group_sum<LPR>(nk) + 1e-6f), rq = rsqrtf(group_sum<LPR>(nq) + 1e-6f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kk[i] *= rk;
+        qq[i] *= rq;
+      }
+    }
+    const float graw = as_f32(x.g);
+    const float alpha = __expf(!LEAN && A_log != nullptr ? -__expf(x.a_log) * softplus(graw + x.dt_bias) : graw);
+    const float bt = as_f32(x.beta);
+    float kq = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kq = fmaf(kk[i], qq[i], kq);
+    kq = group_sum<LPR>(kq);
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      const int row = row0 + j * RPP;
+      float st[8] = {x.s[j][0].x, x.s[j][0].y, x.s[j][0].z, x.s[j][0].w,
+                     x.s[j][1].x, x.s[j][1].y, x.s[j][1].z, x.s[j][1].w};
+      float pk = 0.f, pq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pk = fmaf(st[i], kk[i], pk);
+        pq = fmaf(st[i], qq[i], pq);
+      }
+      pk = group_sum<LPR>(pk);
+      pq = group_sum<LPR>(pq);
+      const float delta = bt * (as_f32(x.vj[j]) - alpha * pk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st[i] = fmaf(delta, kk[i], alpha * st[i]);
+      if (LEAN || row < V) {
+        if (sub == 0) io<TOut>::store(o + (size_t)nh * V + row, scale * fmaf(delta, kq, alpha * pq));
+        if (LEAN || s_out != nullptr) {
+          float* dst = s_out + ((size_t)nh * V + row) * K;
+          *reinterpret_cast<float4*>(dst + c0) = make_float4(st[0], st[1], st[2], st[3]);
+          *reinterpret_cast<float4*>(dst + c1) = make_float4(st[4], st[5], st[6], st[7]);
+        }
+      }
+    }
+  };
+
+  const int stride = gridDim.x * STEP_NWAVES;
+  int ti = blockIdx.x * STEP_NWAVES + wave;
+  if (ti >= n_tiles) return;
+  const int last = n_tiles - 1;
+  Tile b0, b1;
+  load(ti, b0);
+  for (;;) {  // two buffers in turn; every wave leaves after its last tile
+    const int t1 = ti + stride;
+    load(min(t1, last), b1);
+    process(ti, b0);
+    if (t1 >= n_tiles) break;
+    const int t2 = t1 + stride;
+    load(min(t2, last), b0);
+    process(t1, b1);
+    if (t2 >= n_tiles) break;
+    ti = t2;
+  }
+}
+
 struct RecArgs {
   const void *q, *k, *v, *g, *beta;
   const float *A_log, *dt_bias;
@@ -155,8 +323,44 @@ struct RecArgs {
   float scale;
 };
 
+// The single-token step: lean 4-group tiles where there are enough of them for STEP_TILE_WGS_PER_CU
+// workgroups on every CU (about 128 VGPRs: 4 waves per SIMD; 3 workgroups per CU measured fastest), single
+// groups otherwise (small batches, where more waves in flight matter more than q/k reuse) and for the general
+// form, with as many workgroups as fit on a CU at once.
+constexpr int STEP_TILE_WGS_PER_CU = 3;
+
+template <typename TIn, typename TOut, typename TG, int K>
+bool launch_step(const RecArgs& a, hipStream_t stream) {
+  constexpr int RPP = 64 / (K / 8);
+  const long long groups = (long long)a.N * a.Hv * ((a.V + RPP - 1) / RPP);
+  if (groups > INT32_MAX) return false;
+  int dev = 0, n_cu = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    n_cu = 256;
+  n_cu = std::max(1, n_cu);
+  const bool lean = a.s_in != nullptr && a.s_out != nullptr && a.A_log == nullptr && !a.qk_l2norm &&
+                    a.V % RPP == 0;
+  const long long tiles4 = (long long)a.N * a.Hv * (a.V / (4 * RPP));
+  const bool tiled = lean && a.V % (4 * RPP) == 0 && tiles4 >= (long long)STEP_TILE_WGS_PER_CU * n_cu * STEP_NWAVES;
+  const long long n_tiles = tiled ? tiles4 : groups;
+  auto kernel = tiled  ? step_kernel<TIn, TOut, TG, K, true, 4>
+                : lean ? step_kernel<TIn, TOut, TG, K, true, 1>
+                       : step_kernel<TIn, TOut, TG, K, false, 1>;
+  int per_cu = STEP_TILE_WGS_PER_CU;
+  if (!tiled && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * STEP_NWAVES, 0) != hipSuccess ||
+                 per_cu < 1))
+    per_cu = 4;
+  const long long wgs = std::min<long long>((n_tiles + STEP_NWAVES - 1) / STEP_NWAVES, (long long)per_cu * n_cu);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)wgs), dim3(64 * STEP_NWAVES), 0, stream, (const TIn*)a.q,
+                     (const TIn*)a.k, (const TIn*)a.v, (const TG*)a.g, (const TG*)a.beta, a.A_log, a.dt_bias,
+                     a.qk_l2norm, a.s_in, a.s_out, (TOut*)a.o, (int)n_tiles, a.Hk, a.Hv, a.V, a.scale);
+  return true;
+}
+
 template <typename TIn, typename TOut, typename TG, int K>
 void launch(const RecArgs& a, hipStream_t stream) {
+  if (a.T == 1 && a.cu == nullptr && launch_step<TIn, TOut, TG, K>(a, stream)) return;
   constexpr int PASSES = ZGDN_REC_PASSES, NWAVES = ZGDN_REC_NWAVES;
   constexpr int ROWS_WG = (64 / (K / 8)) * PASSES * NWAVES;
   dim3 grid((a.V + ROWS_WG - 1) / ROWS_WG, a.Hv, a.N);
