@@ -50,7 +50,7 @@ def _args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving"], default=None,
                    help="run one workload only (profiling runs); the JSON line then carries that workload")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
@@ -269,6 +269,95 @@ def bench_fused(torch, gdn, steps_per_graph=16):
     }
 
 
+SERVING = dict(hidden=1024, prompt=100, batch_sizes=(2, 32))
+
+
+def _window_replay_step(torch, layer, x, slots, rows, cu, chunks):
+    """The reference's static decode step (servers/sgl/src/zonos3_sgl/models/gdn.py:329-355) through the
+    same operators: the new row goes into the request's 64-row window and the whole window is recomputed
+    from the committed states; states commit when the window fills. The baseline the fast path replaces."""
+    bs, hid = x.shape
+    lens = layer._win_len.index_select(0, slots)
+    pos = rows + lens.long()
+    win = layer._window.index_select(0, slots).view(bs * 64, hid)
+    win.index_copy_(0, pos, x)
+    conv = layer._conv_state.index_select(0, slots)
+    rec = layer._recurrent_state.index_select(0, slots)
+    out, conv_final, final = layer._run_packed(win, cu, chunks, conv, rec)
+    y = out.index_select(0, pos)
+    new_len = (lens + 1) % 64
+    full = new_len == 0
+    layer._conv_state.index_copy_(0, slots, torch.where(full.view(bs, 1, 1), conv_final, conv))
+    layer._recurrent_state.index_copy_(0, slots, torch.where(full.view(bs, 1, 1, 1), final.float(), rec))
+    win = win.view(bs, 64, hid)
+    layer._window.index_copy_(0, slots, torch.where(full.view(bs, 1, 1), torch.zeros_like(win), win))
+    layer._win_len.index_copy_(0, slots, new_len)
+    return y
+
+
+def bench_serving(torch, n_steps=200):
+    """The serving layer's static decode step (OriginalGDN's four heads, hidden 1024, bf16, random weights
+    of the release shapes): one graph-replayed step for bs requests with 100-row prompts, through the fast
+    path (one fused kernel from the live states) and through the reference's window replay."""
+    from types import SimpleNamespace
+
+    serving = importlib.import_module("zonos3-mini_amd.serving")
+    dev = torch.device("cuda:0")
+    hid = SERVING["hidden"]
+    g = torch.Generator(device=dev).manual_seed(1006)
+    bf = torch.bfloat16
+    results = {}
+    for bs in SERVING["batch_sizes"]:
+        batch = SimpleNamespace(is_decode=False, padded_size=bs, gdn_prefill=None)
+        layer = serving.OriginalGDN(SimpleNamespace(hidden_size=hid), 0, batch_source=lambda: batch)
+        layer.in_proj.weight = (0.02 * torch.randn(2056, hid, generator=g, device=dev)).to(bf)
+        layer.conv.weight = (0.2 * torch.randn(1536, 1, 4, generator=g, device=dev)).to(bf)
+        layer.out_weight = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(bf)
+        layer.A_log = 0.2 * torch.randn(4, generator=g, device=dev)
+        layer.dt_bias = 0.2 * torch.randn(4, generator=g, device=dev)
+        layer.wo.weight = (0.02 * torch.randn(hid, 512, generator=g, device=dev)).to(bf)
+        layer.allocate_cache(bs + 1, dev, bf)
+        reqs = [SimpleNamespace(table_idx=i, uid=i, is_cfg_uncond=False, cached_len=0,
+                                device_len=SERVING["prompt"], extend_len=SERVING["prompt"]) for i in range(bs)]
+        batch.reqs = batch.padded_reqs = reqs
+        layer.forward(torch.randn(bs * SERVING["prompt"], hid, generator=g, device=dev).to(bf))
+        slots = torch.arange(bs, device=dev)
+        tables = serving.OriginalGDN.static_tables(dev, [bs])
+        layer.enable_graph_decode(slots, tables)
+        layer.set_static_mode(True)
+        batch.is_decode = True
+        cu, chunks, rows = tables[bs]
+        x = torch.randn(bs, hid, generator=g, device=dev).to(bf)
+        stream = torch.cuda.Stream(dev)
+        timings = {}
+        for name, fn in (("fast_path", lambda: layer.forward(x)),
+                         ("window_replay", lambda: _window_replay_step(torch, layer, x, slots, rows, cu, chunks))):
+            with torch.cuda.stream(stream):
+                fn()
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    fn()
+                for _ in range(10):
+                    graph.replay()
+                torch.cuda.synchronize()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for _ in range(n_steps):
+                    graph.replay()
+                end.record(stream)
+            torch.cuda.synchronize()
+            timings[name] = start.elapsed_time(end) / n_steps * 1e3
+        results[f"bs{bs}"] = {"fast_path_us": round(timings["fast_path"], 2),
+                              "window_replay_us": round(timings["window_replay"], 2),
+                              "speedup": round(timings["window_replay"] / timings["fast_path"], 2)}
+    return {"workload": "serving-layer static decode step, OriginalGDN shapes (4 heads x 128, hidden 1024, "
+                        "in_proj and wo GEMMs included), bf16, 100-row prompts, one step per HIP graph replay: "
+                        "fast path (fused kernel from live states) vs the reference's 64-row window replay "
+                        "through the same operators",
+            **results}
+
+
 def calibrate_copy(torch):
     """10 device copies of 64 MiB (torch's copy kernel): the known-size reference for HBM byte counters."""
     dev = torch.device("cuda:0")
@@ -333,6 +422,9 @@ def main():
         fn = {"prefill": bench_prefill, "varlen": bench_varlen, "fused": bench_fused}[a.only]
         print(json.dumps({"workload_only": a.only, **fn(torch, gdn)}), flush=True)
         return
+    if a.only == "serving":
+        print(json.dumps({"workload_only": a.only, **bench_serving(torch)}), flush=True)
+        return
     dec = bench_decode(torch, gdn, a.steps, a.warmup)
     line = {
         "metric": METRIC,
@@ -370,6 +462,7 @@ def main():
     line["prefill"] = bench_prefill(torch, gdn)
     line["varlen_prefill"] = bench_varlen(torch, gdn)
     line["fused_decode_block"] = bench_fused(torch, gdn)
+    line["serving_decode"] = bench_serving(torch)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
         line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)

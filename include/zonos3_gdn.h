@@ -90,11 +90,36 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
  *   [C, W] (tap 0 oldest); norm_weight [V]; out [B, Hv, V]: all of element type `dtype` (F32 or BF16).
  *   conv_cache [B, C, W-1] (same dtype, oldest first) and state [B, Hv, V, K] (float32) are updated in place.
  *   A_log, dt_bias: float32 [Hv]. K == V == 128, Hv / Hk in {1, 2, 4}.
+ *   qk_round: 0 keeps the L2-normalised q, k in fp32 (lm.py:569-571); nonzero rounds them to `dtype`, as the
+ *   serving layer's l2norm operator returns them (gdn.py:416-417).
  */
 int zgdn_fused_decode_step(const void* x_qkv, const void* z, const void* a, const void* b, int dtype,
                            const void* conv_weight, void* conv_cache, const float* A_log, const float* dt_bias,
                            const void* norm_weight, float* state, void* out, int B, int Hk, int Hv, int K, int V,
-                           int W, float eps, float scale, void* stream);
+                           int W, float eps, float scale, int qk_round, void* stream);
+
+/*
+ * The serving layer's single-row decode step for B requests in table slots, in place on its per-slot caches.
+ * Replaces the static decode of servers/sgl/src/zonos3_sgl/models/gdn.py:329-355, which recomputes each
+ * request's whole 64-row window through the chunked operators (gdn.py:403-445): here the new row goes
+ * through the fused block (zgdn_fused_decode_step's arithmetic) from the slot's live caches.
+ *   mixed [B, mixed_ld]: each request's in_proj row, q|k|v (C = 2 Hk K + Hv V) | z (Hv V) | a (Hv) | b (Hv)
+ *   (the split of gdn.py:402), mixed_ld >= C + Hv V + 2 Hv; x_hidden [B, hidden]: the raw rows; out
+ *   [B, Hv, V]; conv_weight [C, W]; norm_weight [V]: all of element type `dtype`.
+ *   slots [B] int64, distinct: the requests' table slots (one outside [0, n_slots) is skipped: its caches
+ *   are not touched and its out rows are left unwritten). Per slot (n_slots = cap): conv_live, conv_commit
+ *   [cap, C, W] (the last W raw inputs, oldest first, `dtype`); state_live, state_commit [cap, Hv, V, K]
+ *   float32; window [cap, window_rows, hidden] (`dtype`); win_len [cap] int32, the real rows in the window.
+ *   Updates conv_live and state_live; writes the row into window[slot, win_len]; when the window fills
+ *   (win_len + 1 == window_rows) also writes the new conv history and state to conv_commit / state_commit;
+ *   then win_len = (win_len + 1) % window_rows. qk_round as in zgdn_fused_decode_step.
+ */
+int zgdn_serving_decode_step(const void* mixed, long mixed_ld, const void* x_hidden, int hidden, int dtype,
+                             const int64_t* slots, int n_slots, int B, int Hk, int Hv, int K, int V, int W,
+                             const void* conv_weight, void* conv_live, void* conv_commit, float* state_live,
+                             float* state_commit, void* window, int32_t* win_len, int window_rows,
+                             const float* A_log, const float* dt_bias, const void* norm_weight, void* out,
+                             float eps, float scale, int qk_round, void* stream);
 
 /*
  * Depthwise causal conv1d over packed sequences with a rolling history, optional SiLU. Replaces FLA's

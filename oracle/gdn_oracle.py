@@ -199,12 +199,14 @@ def gdn_layer(x, weights: dict, conv_state=None, gdn_state=None, heads=4, head_d
 
 
 def fused_decode_step(x_qkv, z, a, b, conv_w, conv_cache, state, norm_w, A_log, dt_bias, hk, eps=1e-6,
-                      scale=None):
+                      scale=None, round_qk=False):
     """One single-token step of the GDN block for a batch of independent streams (``lm.py:563-587`` with
     T = 1 per stream, grouped value heads).
 
     x_qkv [B, Hk*K + Hk*K + Hv*V] raw projected q|k|v; z [B, Hv, V]; a, b [B, Hv]; conv_w [C, W];
-    conv_cache [B, C, W-1] (oldest first); state [B, Hv, V, K] float32; norm_w [V].
+    conv_cache [B, C, W-1] (oldest first); state [B, Hv, V, K] float32; norm_w [V]. ``round_qk``: the
+    normalised q, k rounded to x's dtype, as the serving layer's l2norm operator returns them
+    (servers/sgl/src/zonos3_sgl/models/gdn.py:416-417).
     Returns (out [B, Hv, V] in x's dtype, new conv cache, new state)."""
     B, C = x_qkv.shape
     hv, V = z.shape[1], z.shape[2]
@@ -216,6 +218,8 @@ def fused_decode_step(x_qkv, z, a, b, conv_w, conv_cache, state, norm_w, A_log, 
         conv = conv[0]
         q = l2norm(conv[: hk * K].reshape(1, hk, K))
         k = l2norm(conv[hk * K : 2 * hk * K].reshape(1, hk, K))
+        if round_qk:
+            q, k = q.to(x_qkv.dtype).float(), k.to(x_qkv.dtype).float()
         v = conv[2 * hk * K :].reshape(1, hv, V).float()
         decay, beta = gate(a[i : i + 1], b[i : i + 1], A_log, dt_bias)
         o, s = gated_delta_sequence(q, k, v, decay, beta, scale, state[i].float())

@@ -23,7 +23,7 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
-            "zgdn_gated_rmsnorm_fwd"} == _declared()
+            "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -83,10 +83,21 @@ def test_bad_arguments_fail_with_a_message(gdn):
     assert lib.zgdn_l2norm_fwd(p, 1, p, 1, None, 4, 2048, 1e-6, None) == native.EUNSUPPORTED
     assert lib.zgdn_gated_rmsnorm_fwd(p, None, p, 1, p, None, 4, 128, 1e-5, None) == native.EINVAL
     assert lib.zgdn_sigmoid_fwd(p, 5, p, 0, 10, 1.0, None) == native.EINVAL
-    fused = [p, p, p, p, 1, p, p, p, p, p, p, p, 2, 1, 8, 128, 128, 4, 1e-6, 1.0, None]
+    fused = [p, p, p, p, 1, p, p, p, p, p, p, p, 2, 1, 8, 128, 128, 4, 1e-6, 1.0, 0, None]
     assert lib.zgdn_fused_decode_step(*fused) == native.EUNSUPPORTED and b"Hv/Hk=8" in lib.zgdn_last_error()
     fused[14], fused[17] = 2, 3
     assert lib.zgdn_fused_decode_step(*fused) == native.EUNSUPPORTED and b"width 3" in lib.zgdn_last_error()
+    # mixed, ld, x, hidden, dtype, slots, n_slots, B, Hk, Hv, K, V, W, conv_w, conv_live, conv_commit, state_live,
+    # state_commit, window, win_len, window_rows, A_log, dt_bias, norm_w, out, eps, scale, qk_round, stream
+    serve = [p, 2056, p, 256, 1, p, 4, 2, 4, 4, 128, 128, 4, p, p, p, p, p, p, p, 64, p, p, p, p, 1e-5, 1.0, 1, None]
+    serve[1] = 2055
+    assert lib.zgdn_serving_decode_step(*serve) == native.EINVAL and b"holds no q|k|v" in lib.zgdn_last_error()
+    serve[1], serve[14] = 2056, None
+    assert lib.zgdn_serving_decode_step(*serve) == native.EINVAL and b"null pointer" in lib.zgdn_last_error()
+    serve[14], serve[9] = p, 32
+    assert lib.zgdn_serving_decode_step(*serve) == native.EUNSUPPORTED and b"Hv/Hk=8" in lib.zgdn_last_error()
+    serve[9], serve[6] = 4, 0
+    assert lib.zgdn_serving_decode_step(*serve) == native.EINVAL and b"n_slots=0" in lib.zgdn_last_error()
 
 
 def test_host_validation_refuses_cpu_tensors(gdn):

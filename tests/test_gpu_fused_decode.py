@@ -31,7 +31,7 @@ def _inputs(B, hk, hv, steps, seed, dtype):
     }
 
 
-def _run_case(gdn, cuda, B, hk, hv, steps, seed, dtype):
+def _run_case(gdn, cuda, B, hk, hv, steps, seed, dtype, round_qk=False):
     d = _inputs(B, hk, hv, steps, seed, dtype)
     dev = {k: v.to(cuda) for k, v in d.items()}
     cache, state = dev["cache"].clone(), dev["s0"].clone()
@@ -39,10 +39,10 @@ def _run_case(gdn, cuda, B, hk, hv, steps, seed, dtype):
     bf16 = dtype == torch.bfloat16
     for t in range(steps):
         out = gdn.fused_decode_step(dev["x"][t], dev["z"][t], dev["a"][t], dev["b"][t], dev["w"], cache, state,
-                                    dev["nw"], dev["A_log"], dev["dt_bias"], eps=1e-6)
+                                    dev["nw"], dev["A_log"], dev["dt_bias"], eps=1e-6, round_qk=round_qk)
         torch.cuda.synchronize()
         o_ref, c_ref, s_ref = O.fused_decode_step(d["x"][t], d["z"][t], d["a"][t], d["b"][t], d["w"], c_ref, s_ref,
-                                                  d["nw"], d["A_log"], d["dt_bias"], hk, eps=1e-6)
+                                                  d["nw"], d["A_log"], d["dt_bias"], hk, eps=1e-6, round_qk=round_qk)
         assert torch.equal(cache.cpu(), c_ref), f"conv cache differs at step {t}"
         if bf16:
             assert max_abs(out.cpu(), o_ref) < 2e-2, (t, max_abs(out.cpu(), o_ref))
@@ -62,6 +62,23 @@ def test_streaming_block_B256_Hk8_Hv16(gdn, cuda):
 def test_group_sizes_bf16(gdn, cuda, hk, hv):
     announce(f"fused decode B=5 Hk={hk} Hv={hv} bf16 x4 steps")
     _run_case(gdn, cuda, 5, hk, hv, 4, seed=5100 + hv, dtype=torch.bfloat16)
+
+
+def test_rounded_qk_like_the_serving_operators(gdn, cuda):
+    """round_qk: the normalised q, k rounded to bf16 (the serving layer's l2norm operator output); the
+    serving layer's head shape (4 q/k heads, 4 v heads). The rounding changes the state (so it is applied)."""
+    announce("fused decode B=6 Hk=Hv=4 bf16 x4 steps, q/k rounded")
+    _run_case(gdn, cuda, 6, 4, 4, 4, seed=5300, dtype=torch.bfloat16, round_qk=True)
+    d = _inputs(2, 4, 4, 1, 5301, torch.bfloat16)
+    dev = {k: v.to(cuda) for k, v in d.items()}
+    states = []
+    for r in (False, True):
+        cache, state = dev["cache"].clone(), dev["s0"].clone()
+        gdn.fused_decode_step(dev["x"][0], dev["z"][0], dev["a"][0], dev["b"][0], dev["w"], cache, state,
+                              dev["nw"], dev["A_log"], dev["dt_bias"], round_qk=r)
+        states.append(state)
+    torch.cuda.synchronize()
+    assert not torch.equal(states[0], states[1])
 
 
 def test_float32_block(gdn, cuda):

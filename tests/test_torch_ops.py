@@ -10,8 +10,8 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 from gdn_testing import announce
 from oracle import gdn_oracle as O
 
-OPS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "causal_conv1d", "l2norm", "sigmoid",
-       "gated_rmsnorm")
+OPS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step", "causal_conv1d",
+       "l2norm", "sigmoid", "gated_rmsnorm")
 
 
 def test_registered_with_mutation_annotations(gdn):
@@ -24,7 +24,10 @@ def test_registered_with_mutation_annotations(gdn):
     }
     assert mutated["decode_step"] == {"state"}
     assert mutated["fused_decode_step"] == {"conv_cache", "state"}
-    assert all(not m for n, m in mutated.items() if n not in ("decode_step", "fused_decode_step"))
+    assert mutated["serving_decode_step"] == {"conv_live", "conv_commit", "state_live", "state_commit", "window",
+                                              "win_len"}
+    assert all(not m for n, m in mutated.items()
+               if n not in ("decode_step", "fused_decode_step", "serving_decode_step"))
 
 
 def test_fake_shapes(gdn):
@@ -51,6 +54,14 @@ def test_fake_shapes(gdn):
         nw = torch.empty(128, dtype=torch.bfloat16)
         hv = torch.empty(4)
         assert z.fused_decode_step(x, zz, ab, ab, w, cache, st6, nw, hv, hv).shape == (6, 4, 128)
+        mixed = torch.empty(3, 2056, dtype=torch.bfloat16)
+        conv4 = torch.empty(5, 1536, 4, dtype=torch.bfloat16)
+        st5 = torch.empty(5, 4, 128, 128)
+        win = torch.empty(5, 64, 256, dtype=torch.bfloat16)
+        y = z.serving_decode_step(mixed, torch.empty(3, 256, dtype=torch.bfloat16), torch.empty(3, dtype=torch.long),
+                                  torch.empty(1536, 4, dtype=torch.bfloat16), conv4, conv4, st5, st5, win,
+                                  torch.empty(5, dtype=torch.int32), nw, hv, hv)
+        assert y.shape == (3, 4, 128) and y.dtype == torch.bfloat16
         xc = torch.empty(1, 130, 96)
         y, fin = z.causal_conv1d(xc, torch.empty(96, 4), None, None, cu, None, "silu", 3)
         assert y.shape == xc.shape and fin.shape == (3, 96, 3)

@@ -8,7 +8,7 @@ There is no fallback: a missing or unloadable library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_long, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libzonos3_gdn.so"
@@ -39,7 +39,12 @@ SIGNATURES: dict[str, tuple] = {
     "zgdn_fused_decode_step": (
         c_int,
         [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P,
-         c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P],
+         c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, _P],
+    ),
+    "zgdn_serving_decode_step": (
+        c_int,
+        [_P, c_long, _P, c_int, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+         _P, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_float, c_float, c_int, _P],
     ),
     "zgdn_causal_conv1d_fwd": (
         c_int,

@@ -4,7 +4,9 @@
 // The reference statement is model/src/zonos3/reference/lm.py:563-587 applied to one new row per stream:
 //   conv   = silu(conv1d([history | x]))       computed in fp32, rounded to the input dtype after the conv and
 //                                              after the SiLU (F.conv1d / F.silu on x.dtype tensors)
-//   q, k   = l2norm(conv_q), l2norm(conv_k)    fp32, x * rsqrt(sum x^2 + 1e-6)
+//   q, k   = l2norm(conv_q), l2norm(conv_k)    fp32, x * rsqrt(sum x^2 + 1e-6); with qk_round rounded to the
+//                                              input dtype, as the serving layer's l2norm operator returns
+//                                              them (servers/sgl/src/zonos3_sgl/models/gdn.py:416-417)
 //   decay  = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)
 //   S      = decay S; d = beta (v - S k); S += d k^T; o = S (q scale)     (fp32 state [Hv, V, K])
 //   out    = (rms_norm(o.to(dtype)) * w).to(dtype) * silu(z), product in fp32, cast to dtype
@@ -15,6 +17,8 @@
 // loads of their state rows (G * 128 rows of 512 B), then form the conv / norms / gates of the group in LDS,
 // then update the rows exactly like the recurrent kernel (16 lanes per row, DPP row reductions) and finish
 // with the per-head gated RMSNorm.
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace zgdn {
@@ -33,12 +37,40 @@ __device__ __forceinline__ float round_to(float x) {
   else return x;
 }
 
-template <typename T, int G>
-__global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(
-    const T* __restrict__ x, const T* __restrict__ z, const T* __restrict__ a, const T* __restrict__ b,
-    const T* __restrict__ conv_w, T* __restrict__ conv_cache, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, const T* __restrict__ norm_w, float* __restrict__ state, T* __restrict__ out,
-    int Hk, int Hv, float eps, float scale) {
+// Where a launch reads and writes. The plain block step: stream b's rows at b, conv cache [B, C, W-1].
+// The serving step: stream b's q|k|v, z, a, b are slices of one in_proj row, its caches are those of table
+// slot slots[b] (conv history [cap, C, W], the FLA layout), and a window that fills up commits the new
+// conv history and state to the committed caches.
+template <typename T>
+struct FusedArgs {
+  const T* x;          // q|k|v channels of stream b at x + b * x_ld
+  const T* z;          // z of stream b at z + b * z_ld, [Hv, V]
+  const T* a;          // a, b of stream b at a/b + b * ab_ld, [Hv]
+  const T* b;
+  long x_ld, z_ld, ab_ld;
+  const T* conv_w;     // [C, W]
+  T* conv_cache;       // [rows, C, CW]: the last CW raw inputs, oldest first
+  const float* A_log;
+  const float* dt_bias;
+  const T* norm_w;
+  float* state;        // [rows, Hv, V, K]
+  T* out;              // [B, Hv, V]
+  const int64_t* slots;     // serving: rows of stream b; rows outside [0, n_rows) are skipped (else row b)
+  long n_rows;
+  const int32_t* win_len;   // serving: real rows in each slot's window before this step
+  T* conv_commit;           // serving: committed caches, written when the window fills
+  float* state_commit;
+  T* window;                // serving: [rows, window_rows, hidden] raw rows; receives stream b's row
+  const T* x_hidden;        // [B, hidden]
+  int hidden, window_rows;
+  int Hk, Hv;
+  float eps, scale;
+  int qk_round;
+};
+
+template <typename T, int G, int CW>
+__global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const FusedArgs<T> p) {
+  constexpr bool SERVING = CW == FD_W;  // slot-indexed caches, window and commits (the serving step)
   constexpr int PASSES = G * FD_K / FD_ROWS_PASS;  // 4 per value head
   constexpr int NCH = 2 * FD_K + G * FD_K;         // conv channels of the group
   __shared__ float s_conv[NCH];                    // q | k | v_0 .. v_{G-1} after conv + SiLU (+ L2 for q, k)
@@ -46,49 +78,76 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(
   __shared__ float s_red[FD_WAVES][1];
   __shared__ float s_gate[G][2];
 
+  const int Hk = p.Hk, Hv = p.Hv;
   const int bs = blockIdx.x / Hk, hk = blockIdx.x % Hk;
+  long srow = bs;
+  if constexpr (SERVING) {
+    srow = p.slots[bs];
+    if (srow < 0 || srow >= p.n_rows) return;  // a slot outside the caches: nothing is read or written
+  }
+  const size_t row = (size_t)srow;
   const int C = 2 * Hk * FD_K + Hv * FD_K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane % FD_LPR, rsub = lane / FD_LPR;
   const int c0 = sub * 4, c1 = FD_K / 2 + sub * 4;
-
-  // 0. issue the state loads of this lane's rows (row r = pass * 32 + wave * 4 + rsub; head r / 128)
-  float* sgroup = state + ((size_t)bs * Hv + (size_t)hk * G) * FD_K * FD_K;
-  float s[PASSES][8];
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int r = p * FD_ROWS_PASS + wave * FD_RPP + rsub;
-    const float* src = sgroup + (size_t)r * FD_K;
-    const float4 u = io<float>::load4(src + c0), w = io<float>::load4(src + c1);
-    s[p][0] = u.x; s[p][1] = u.y; s[p][2] = u.z; s[p][3] = u.w;
-    s[p][4] = w.x; s[p][5] = w.y; s[p][6] = w.z; s[p][7] = w.w;
+  int wlen = 0;
+  bool commit = false;
+  if constexpr (SERVING) {
+    wlen = p.win_len[row];
+    commit = wlen + 1 == p.window_rows;
   }
 
-  // 1. conv + SiLU of the group's channels; the rolling history becomes (h1, h2, x)
+  // 0. issue the state loads of this lane's rows (row r = pass * 32 + wave * 4 + rsub; head r / 128)
+  const size_t group_off = (row * Hv + (size_t)hk * G) * FD_K * FD_K;
+  float* sgroup = p.state + group_off;
+  float s[PASSES][8];
+#pragma unroll
+  for (int q = 0; q < PASSES; ++q) {
+    const int r = q * FD_ROWS_PASS + wave * FD_RPP + rsub;
+    const float* src = sgroup + (size_t)r * FD_K;
+    const float4 u = io<float>::load4(src + c0), w = io<float>::load4(src + c1);
+    s[q][0] = u.x; s[q][1] = u.y; s[q][2] = u.z; s[q][3] = u.w;
+    s[q][4] = w.x; s[q][5] = w.y; s[q][6] = w.z; s[q][7] = w.w;
+  }
+
+  // 1. conv + SiLU of the group's channels; the history rolls by one (the oldest input drops out)
   for (int i = tid; i < NCH; i += 64 * FD_WAVES) {
     int ch;
     if (i < FD_K) ch = hk * FD_K + i;                                     // q
     else if (i < 2 * FD_K) ch = Hk * FD_K + hk * FD_K + (i - FD_K);       // k
     else ch = 2 * Hk * FD_K + hk * G * FD_K + (i - 2 * FD_K);             // v of heads hk*G ..
-    const size_t xc = (size_t)bs * C + ch;
-    T* hist = conv_cache + xc * (FD_W - 1);
-    const float xv = io<T>::load(x + xc);
+    const size_t hc = (row * C + ch) * CW;
+    T* hist = p.conv_cache + hc + (CW - (FD_W - 1));  // the taps' history: the last W-1 columns
+    const float xv = io<T>::load(p.x + bs * p.x_ld + ch);
     const float h0 = io<T>::load(hist), h1 = io<T>::load(hist + 1), h2 = io<T>::load(hist + 2);
-    const T* w = conv_w + (size_t)ch * FD_W;
+    const T* w = p.conv_w + (size_t)ch * FD_W;
     float acc = io<T>::load(w) * h0;
     acc = fmaf(io<T>::load(w + 1), h1, acc);
     acc = fmaf(io<T>::load(w + 2), h2, acc);
     acc = fmaf(io<T>::load(w + 3), xv, acc);
     s_conv[i] = round_to<T>(silu(round_to<T>(acc)));
-    io<T>::store(hist, h1);
-    io<T>::store(hist + 1, h2);
-    io<T>::store(hist + 2, xv);
+    T* dst = p.conv_cache + hc;
+    if constexpr (CW == FD_W) io<T>::store(dst++, h0);  // a full-width history keeps h0 as its oldest input
+    io<T>::store(dst, h1);
+    io<T>::store(dst + 1, h2);
+    io<T>::store(dst + 2, xv);
+    if (SERVING && commit) {
+      T* cdst = p.conv_commit + hc;
+      if constexpr (CW == FD_W) io<T>::store(cdst++, h0);
+      io<T>::store(cdst, h1);
+      io<T>::store(cdst + 1, h2);
+      io<T>::store(cdst + 2, xv);
+    }
   }
   if (tid < G) {
     const int h = hk * G + tid;
-    const size_t gi = (size_t)bs * Hv + h;
-    s_gate[tid][0] = __expf(-__expf(A_log[h]) * softplus(io<T>::load(a + gi) + dt_bias[h]));
-    s_gate[tid][1] = sigmoid(io<T>::load(b + gi));
+    s_gate[tid][0] = __expf(-__expf(p.A_log[h]) * softplus(io<T>::load(p.a + bs * p.ab_ld + h) + p.dt_bias[h]));
+    s_gate[tid][1] = sigmoid(io<T>::load(p.b + bs * p.ab_ld + h));
+  }
+  if (SERVING && hk == 0 && wlen >= 0 && wlen < p.window_rows) {  // the raw row joins the slot's window
+    T* wrow = p.window + (row * p.window_rows + wlen) * p.hidden;
+    const T* xrow = p.x_hidden + (size_t)bs * p.hidden;
+    for (int i = tid; i < p.hidden; i += 64 * FD_WAVES) wrow[i] = xrow[i];
   }
   __syncthreads();
 
@@ -98,8 +157,8 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(
     const float x0 = v[lane], x1 = v[lane + 64];
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float r = rsqrtf(ss + 1e-6f);
-    v[lane] = x0 * r;
-    v[lane + 64] = x1 * r;
+    v[lane] = p.qk_round ? round_to<T>(x0 * r) : x0 * r;
+    v[lane + 64] = p.qk_round ? round_to<T>(x1 * r) : x1 * r;
   }
   __syncthreads();
 
@@ -118,26 +177,33 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(
   for (int i = 0; i < 8; ++i) kq = fmaf(kk[i], qq[i], kq);
   kq = group_sum<FD_LPR>(kq);
 #pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int r = p * FD_ROWS_PASS + wave * FD_RPP + rsub;
+  for (int q = 0; q < PASSES; ++q) {
+    const int r = q * FD_ROWS_PASS + wave * FD_RPP + rsub;
     const int g = r / FD_K, j = r % FD_K;
     const float alpha = s_gate[g][0], bt = s_gate[g][1];
     const float vj = s_conv[2 * FD_K + r];
     float pk = 0.f, pq = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      pk = fmaf(s[p][i], kk[i], pk);
-      pq = fmaf(s[p][i], qq[i], pq);
+      pk = fmaf(s[q][i], kk[i], pk);
+      pq = fmaf(s[q][i], qq[i], pq);
     }
     pk = group_sum<FD_LPR>(pk);
     pq = group_sum<FD_LPR>(pq);
     const float delta = bt * (vj - alpha * pk);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s[p][i] = fmaf(delta, kk[i], alpha * s[p][i]);
+    for (int i = 0; i < 8; ++i) s[q][i] = fmaf(delta, kk[i], alpha * s[q][i]);
+    const float4 n0 = make_float4(s[q][0], s[q][1], s[q][2], s[q][3]);
+    const float4 n1 = make_float4(s[q][4], s[q][5], s[q][6], s[q][7]);
     float* dst = sgroup + (size_t)r * FD_K;
-    io<float>::store4(dst + c0, make_float4(s[p][0], s[p][1], s[p][2], s[p][3]));
-    io<float>::store4(dst + c1, make_float4(s[p][4], s[p][5], s[p][6], s[p][7]));
-    if (sub == 0) s_o[g][j] = scale * fmaf(delta, kq, alpha * pq);
+    io<float>::store4(dst + c0, n0);
+    io<float>::store4(dst + c1, n1);
+    if (SERVING && commit) {
+      float* cdst = p.state_commit + group_off + (size_t)r * FD_K;
+      io<float>::store4(cdst + c0, n0);
+      io<float>::store4(cdst + c1, n1);
+    }
+    if (sub == 0) s_o[g][j] = p.scale * fmaf(delta, kq, alpha * pq);
   }
   __syncthreads();
 
@@ -154,29 +220,67 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(
     const int h = hk * G + g;
     const float ov = round_to<T>(s_o[g][j]);
     const float ms = (s_red[2 * g][0] + s_red[2 * g + 1][0]) / (float)FD_K;
-    const float nrm = round_to<T>(ov * rsqrtf(ms + eps) * io<T>::load(norm_w + j));
-    const size_t zi = ((size_t)bs * Hv + h) * FD_K + j;
-    io<T>::store(out + zi, nrm * silu(io<T>::load(z + zi)));
+    const float nrm = round_to<T>(ov * rsqrtf(ms + p.eps) * io<T>::load(p.norm_w + j));
+    const float zv = io<T>::load(p.z + bs * p.z_ld + (size_t)h * FD_K + j);
+    io<T>::store(p.out + ((size_t)bs * Hv + h) * FD_K + j, nrm * silu(zv));
   }
 }
 
-template <typename T>
-void launch_fused(int G, int B, int Hk, int Hv, const void* x, const void* z, const void* a, const void* b,
-                  const void* conv_w, void* conv_cache, const float* A_log, const float* dt_bias, const void* norm_w,
-                  float* state, void* out, float eps, float scale, hipStream_t stream) {
-  dim3 grid(B * Hk), block(64 * FD_WAVES);
-#define ZGDN_FUSED_CASE(GG)                                                                                     \
-  case GG:                                                                                                      \
-    hipLaunchKernelGGL((fused_decode_kernel<T, GG>), grid, block, 0, stream, (const T*)x, (const T*)z,         \
-                       (const T*)a, (const T*)b, (const T*)conv_w, (T*)conv_cache, A_log, dt_bias,             \
-                       (const T*)norm_w, state, (T*)out, Hk, Hv, eps, scale);                                  \
-    break;
-  switch (G) {
-    ZGDN_FUSED_CASE(1)
-    ZGDN_FUSED_CASE(2)
-    ZGDN_FUSED_CASE(4)
+// Each listed slot's window gains the row just written: win_len = (win_len + 1) % window_rows.
+__global__ void advance_windows_kernel(const int64_t* __restrict__ slots, int32_t* __restrict__ win_len, int B,
+                                       long n_rows, int window_rows) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < B && slots[i] >= 0 && slots[i] < n_rows) {
+    int32_t* w = win_len + slots[i];
+    *w = (*w + 1) % window_rows;
   }
-#undef ZGDN_FUSED_CASE
+}
+
+template <typename T, int CW>
+void launch_fused(int G, int B, const FusedArgs<T>& p, hipStream_t stream) {
+  dim3 grid(B * p.Hk), block(64 * FD_WAVES);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((fused_decode_kernel<T, 1, CW>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((fused_decode_kernel<T, 2, CW>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((fused_decode_kernel<T, 4, CW>), grid, block, 0, stream, p); break;
+  }
+}
+
+int check_fused_sizes(const char* fn, int B, int Hk, int Hv, int K, int V, int W, int dtype) {
+  if (K != FD_K || V != FD_K) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d V=%d (supported: 128)", fn, K, V);
+  if (W != FD_W) return fail(ZGDN_EUNSUPPORTED, "%s: conv width %d (supported: 4)", fn, W);
+  if (B < 1 || Hk < 1 || Hv < 1 || Hv % Hk) return fail(ZGDN_EINVAL, "%s: bad sizes B=%d Hk=%d Hv=%d", fn, B, Hk, Hv);
+  const int G = Hv / Hk;
+  if (G != 1 && G != 2 && G != 4) return fail(ZGDN_EUNSUPPORTED, "%s: Hv/Hk=%d (supported: 1, 2, 4)", fn, G);
+  if (dtype != ZGDN_F32 && dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, dtype);
+  return ZGDN_OK;
+}
+
+template <typename T>
+FusedArgs<T> plain_args(const void* x_qkv, const void* z, const void* a, const void* b, const void* conv_weight,
+                        void* conv_cache, const float* A_log, const float* dt_bias, const void* norm_weight,
+                        float* state, void* out, int Hk, int Hv, float eps, float scale, int qk_round) {
+  FusedArgs<T> p{};
+  p.x = (const T*)x_qkv;
+  p.z = (const T*)z;
+  p.a = (const T*)a;
+  p.b = (const T*)b;
+  p.x_ld = 2L * Hk * FD_K + (long)Hv * FD_K;
+  p.z_ld = (long)Hv * FD_K;
+  p.ab_ld = Hv;
+  p.conv_w = (const T*)conv_weight;
+  p.conv_cache = (T*)conv_cache;
+  p.A_log = A_log;
+  p.dt_bias = dt_bias;
+  p.norm_w = (const T*)norm_weight;
+  p.state = state;
+  p.out = (T*)out;
+  p.Hk = Hk;
+  p.Hv = Hv;
+  p.eps = eps;
+  p.scale = scale;
+  p.qk_round = qk_round;
+  return p;
 }
 
 }  // namespace
@@ -186,24 +290,82 @@ extern "C" int zgdn_fused_decode_step(const void* x_qkv, const void* z, const vo
                                       const void* conv_weight, void* conv_cache, const float* A_log,
                                       const float* dt_bias, const void* norm_weight, float* state, void* out,
                                       int B, int Hk, int Hv, int K, int V, int W, float eps, float scale,
-                                      void* stream) {
+                                      int qk_round, void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_fused_decode_step";
   if (!x_qkv || !z || !a || !b || !conv_weight || !conv_cache || !A_log || !dt_bias || !norm_weight || !state ||
       !out)
     return fail(ZGDN_EINVAL, "%s: null pointer", fn);
-  if (K != FD_K || V != FD_K) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d V=%d (supported: 128)", fn, K, V);
-  if (W != FD_W) return fail(ZGDN_EUNSUPPORTED, "%s: conv width %d (supported: 4)", fn, W);
-  if (B < 1 || Hk < 1 || Hv < 1 || Hv % Hk) return fail(ZGDN_EINVAL, "%s: bad sizes B=%d Hk=%d Hv=%d", fn, B, Hk, Hv);
+  if (int rc = check_fused_sizes(fn, B, Hk, Hv, K, V, W, dtype)) return rc;
   const int G = Hv / Hk;
-  if (G != 1 && G != 2 && G != 4) return fail(ZGDN_EUNSUPPORTED, "%s: Hv/Hk=%d (supported: 1, 2, 4)", fn, G);
-  if (dtype != ZGDN_F32 && dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, dtype);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == ZGDN_F32)
-    launch_fused<float>(G, B, Hk, Hv, x_qkv, z, a, b, conv_weight, conv_cache, A_log, dt_bias, norm_weight, state,
-                        out, eps, scale, s);
+    launch_fused<float, FD_W - 1>(G, B, plain_args<float>(x_qkv, z, a, b, conv_weight, conv_cache, A_log, dt_bias,
+                                                          norm_weight, state, out, Hk, Hv, eps, scale, qk_round), s);
   else
-    launch_fused<bf16>(G, B, Hk, Hv, x_qkv, z, a, b, conv_weight, conv_cache, A_log, dt_bias, norm_weight, state,
-                       out, eps, scale, s);
+    launch_fused<bf16, FD_W - 1>(G, B, plain_args<bf16>(x_qkv, z, a, b, conv_weight, conv_cache, A_log, dt_bias,
+                                                        norm_weight, state, out, Hk, Hv, eps, scale, qk_round), s);
+  return check_launch(fn);
+}
+
+extern "C" int zgdn_serving_decode_step(const void* mixed, long mixed_ld, const void* x_hidden, int hidden,
+                                        int dtype, const int64_t* slots, int n_slots, int B, int Hk, int Hv, int K,
+                                        int V, int W,
+                                        const void* conv_weight, void* conv_live, void* conv_commit,
+                                        float* state_live, float* state_commit, void* window, int32_t* win_len,
+                                        int window_rows, const float* A_log, const float* dt_bias,
+                                        const void* norm_weight, void* out, float eps, float scale, int qk_round,
+                                        void* stream) {
+  using namespace zgdn;
+  const char* fn = "zgdn_serving_decode_step";
+  if (!mixed || !x_hidden || !slots || !conv_weight || !conv_live || !conv_commit || !state_live ||
+      !state_commit || !window || !win_len || !A_log || !dt_bias || !norm_weight || !out)
+    return fail(ZGDN_EINVAL, "%s: null pointer", fn);
+  if (int rc = check_fused_sizes(fn, B, Hk, Hv, K, V, W, dtype)) return rc;
+  const long C = 2L * Hk * K + (long)Hv * V;
+  if (mixed_ld < C + (long)Hv * V + 2L * Hv)
+    return fail(ZGDN_EINVAL, "%s: in_proj row of %ld elements holds no q|k|v (%ld), z (%d), a, b (%d each)", fn,
+                mixed_ld, C, Hv * V, Hv);
+  if (hidden < 1 || window_rows < 1 || n_slots < 1)
+    return fail(ZGDN_EINVAL, "%s: hidden=%d window_rows=%d n_slots=%d", fn, hidden, window_rows, n_slots);
+  const int G = Hv / Hk;
+  hipStream_t s = (hipStream_t)stream;
+  auto fill = [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    FusedArgs<T> p{};
+    p.x = (const T*)mixed;
+    p.z = p.x + C;
+    p.a = p.z + (long)Hv * V;
+    p.b = p.a + Hv;
+    p.x_ld = p.z_ld = p.ab_ld = mixed_ld;
+    p.conv_w = (const T*)conv_weight;
+    p.conv_cache = (T*)conv_live;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.norm_w = (const T*)norm_weight;
+    p.state = state_live;
+    p.out = (T*)out;
+    p.slots = slots;
+    p.n_rows = n_slots;
+    p.win_len = win_len;
+    p.conv_commit = (T*)conv_commit;
+    p.state_commit = state_commit;
+    p.window = (T*)window;
+    p.x_hidden = (const T*)x_hidden;
+    p.hidden = hidden;
+    p.window_rows = window_rows;
+    p.Hk = Hk;
+    p.Hv = Hv;
+    p.eps = eps;
+    p.scale = scale;
+    p.qk_round = qk_round;
+    launch_fused<T, FD_W>(G, B, p, s);
+  };
+  if (dtype == ZGDN_F32)
+    fill((float*)nullptr);
+  else
+    fill((bf16*)nullptr);
+  hipLaunchKernelGGL(advance_windows_kernel, dim3((B + 255) / 256), dim3(256), 0, s, slots, win_len, B,
+                     (long)n_slots, window_rows);
   return check_launch(fn);
 }

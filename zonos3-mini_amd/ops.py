@@ -197,13 +197,15 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
 
 
 def fused_decode_step(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weight, A_log, dt_bias, eps=1e-6,
-                      scale=None):
+                      scale=None, round_qk=False):
     """One single-token step of the whole GDN block for B streams (lm.py:563-587 for one new row each).
 
     x_qkv [B, 2*Hk*128 + Hv*128] raw q|k|v channels; z [B, Hv, 128]; a, b [B, Hv] (raw gate inputs);
     conv_weight [C, 4] or [C, 1, 4]; norm_weight [128] -- all bfloat16 or all float32. conv_cache [B, C, 3]
     (same dtype, oldest first) and state [B, Hv, 128, 128] float32 are updated in place; A_log, dt_bias
-    float32 [Hv]. Returns the gated, normalised output [B, Hv, 128]."""
+    float32 [Hv]. ``round_qk``: round the L2-normalised q, k to the input dtype (the serving layer's l2norm
+    operator returns them so, gdn.py:416-417) instead of keeping them fp32 (lm.py:569-571). Returns the gated,
+    normalised output [B, Hv, 128]."""
     _on_gpu("x_qkv", x_qkv)
     dev = x_qkv.device
     _require(x_qkv.dim() == 2, f"x_qkv: expected [B, C], got {tuple(x_qkv.shape)}")
@@ -236,7 +238,69 @@ def fused_decode_step(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weigh
     _native.call(
         "zgdn_fused_decode_step", x_qkv.data_ptr(), z.data_ptr(), a.data_ptr(), b.data_ptr(), _code(x_qkv, "x_qkv"),
         conv_weight.data_ptr(), conv_cache.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), norm_weight.data_ptr(),
-        state.data_ptr(), out.data_ptr(), B, Hk, Hv, K, V, 4, float(eps), scale, _stream(dev),
+        state.data_ptr(), out.data_ptr(), B, Hk, Hv, K, V, 4, float(eps), scale, int(bool(round_qk)), _stream(dev),
+    )
+    return out
+
+
+def serving_decode_step(mixed, x_hidden, slots, conv_weight, conv_live, conv_commit, state_live, state_commit,
+                        window, win_len, norm_weight, A_log, dt_bias, eps=1e-5, scale=None, round_qk=True):
+    """The serving layer's single-row decode for B requests in table slots, in place on the per-slot caches
+    (the fast path of ``servers/sgl/src/zonos3_sgl/models/gdn.py:329-355``; C ABI ``zgdn_serving_decode_step``).
+
+    mixed [B, >= C + Hv*128 + 2*Hv] in_proj rows (q|k|v | z | a | b, unit stride within a row); x_hidden
+    [B, hidden] the raw rows; slots int64 [B], distinct table slots. Caches over ``cap`` slots: conv_live,
+    conv_commit [cap, C, 4] and window [cap, R, hidden] in mixed's dtype; state_live, state_commit
+    [cap, Hv, 128, 128] float32; win_len int32 [cap]. conv_weight [C, 4] or [C, 1, 4], norm_weight [128] in
+    mixed's dtype; A_log, dt_bias float32 [Hv]. Returns the gated, normalised output [B, Hv, 128]."""
+    _on_gpu("mixed", mixed)
+    dev = mixed.device
+    _require(mixed.dim() == 2 and mixed.stride(1) == 1, f"mixed: expected [B, L] rows, got {tuple(mixed.shape)}")
+    B = mixed.shape[0]
+    _require(conv_live.dim() == 3, f"conv_live: expected [cap, C, 4], got {tuple(conv_live.shape)}")
+    cap, C, W = conv_live.shape
+    _require(W == 4, f"conv_live: conv width {W} (supported: 4)")
+    _require(state_live.dim() == 4 and state_live.shape[0] == cap and state_live.shape[2:] == (128, 128),
+             f"state_live: expected [{cap}, Hv, 128, 128], got {tuple(state_live.shape)}")
+    Hv, K = state_live.shape[1], 128
+    _require((C - Hv * K) > 0 and (C - Hv * K) % (2 * K) == 0, f"conv_live: {C} channels do not split into "
+                                                                f"q|k|v with Hv={Hv}, head size {K}")
+    Hk = (C - Hv * K) // (2 * K)
+    _require(mixed.shape[1] >= C + Hv * K + 2 * Hv, f"mixed: {mixed.shape[1]} columns hold no q|k|v ({C}), z "
+                                                    f"({Hv * K}), a, b ({Hv} each)")
+    if conv_weight.dim() == 3:
+        conv_weight = conv_weight.squeeze(1)
+    dt = mixed.dtype
+    _require(window.dim() == 3 and window.shape[0] == cap, f"window: expected [{cap}, R, hidden]")
+    hidden = window.shape[2]
+    for name, t, shape in (("x_hidden", x_hidden, (B, hidden)), ("conv_weight", conv_weight, (C, 4)),
+                           ("conv_live", conv_live, (cap, C, 4)), ("norm_weight", norm_weight, (K,)),
+                           ("window", window, tuple(window.shape))):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == dt, f"{name}: dtype {t.dtype}, expected {dt} (the dtype of mixed)")
+        _require(tuple(t.shape) == shape and t.is_contiguous(), f"{name}: expected contiguous {list(shape)}")
+    _on_gpu("conv_commit", conv_commit, dev)
+    _require(conv_commit.dtype == dt and conv_commit.shape == conv_live.shape and conv_commit.is_contiguous()
+             and conv_live.is_contiguous(), f"conv_live, conv_commit: contiguous {dt} [{cap}, {C}, 4]")
+    for name, t in (("state_live", state_live), ("state_commit", state_commit)):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == torch.float32 and t.shape == (cap, Hv, K, K) and t.is_contiguous(),
+                 f"{name}: expected contiguous float32 [{cap}, {Hv}, {K}, {K}]")
+    _on_gpu("slots", slots, dev)
+    _require(slots.dtype == torch.int64 and slots.shape == (B,) and slots.is_contiguous(), f"slots: int64 [{B}]")
+    _on_gpu("win_len", win_len, dev)
+    _require(win_len.dtype == torch.int32 and win_len.shape == (cap,), f"win_len: int32 [{cap}]")
+    for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
+    out = torch.empty(B, Hv, K, device=dev, dtype=dt)
+    scale = K**-0.5 if scale is None else float(scale)
+    _native.call(
+        "zgdn_serving_decode_step", mixed.data_ptr(), mixed.stride(0), x_hidden.data_ptr(), hidden,
+        _code(mixed, "mixed"), slots.data_ptr(), cap, B, Hk, Hv, K, K, 4, conv_weight.data_ptr(),
+        conv_live.data_ptr(), conv_commit.data_ptr(), state_live.data_ptr(), state_commit.data_ptr(),
+        window.data_ptr(), win_len.data_ptr(), window.shape[1], A_log.data_ptr(), dt_bias.data_ptr(),
+        norm_weight.data_ptr(), out.data_ptr(), float(eps), scale, int(bool(round_qk)), _stream(dev),
     )
     return out
 

@@ -12,6 +12,7 @@ state in place declare it in ``mutates_args``.
 | ``zgdn::decode_step`` | one lm.py:574-583 step for B streams, state in place |
 | ``zgdn::chunk_fwd`` | FLA ``chunk_gated_delta_rule_fwd`` (gdn.py:418-434) |
 | ``zgdn::fused_decode_step`` | lm.py:563-587 for one new row per stream, conv cache and state in place |
+| ``zgdn::serving_decode_step`` | the serving layer's static decode (gdn.py:329-355) on per-slot caches in place |
 | ``zgdn::causal_conv1d`` | FLA ``causal_conv1d_fwd`` (gdn.py:403-414); lm.py:563-568 |
 | ``zgdn::l2norm`` | FLA ``l2norm_fwd`` (gdn.py:416-417); lm.py:570-571 |
 | ``zgdn::sigmoid`` | FLA ``fused_beta_sigmoid_fwd`` (gdn.py:423); lm.py:573 |
@@ -93,14 +94,32 @@ def _(q, k, v, g, beta, scale=None, initial_state=None, cu_seqlens=None, chunk_i
 @torch.library.custom_op(f"{NS}::fused_decode_step", mutates_args=("conv_cache", "state"))
 def fused_decode_step(x_qkv: Tensor, z: Tensor, a: Tensor, b: Tensor, conv_weight: Tensor, conv_cache: Tensor,
                       state: Tensor, norm_weight: Tensor, A_log: Tensor, dt_bias: Tensor, eps: float = 1e-6,
-                      scale: Optional[float] = None) -> Tensor:
+                      scale: Optional[float] = None, round_qk: bool = False) -> Tensor:
     return ops.fused_decode_step(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weight, A_log, dt_bias,
-                                 eps=eps, scale=scale)
+                                 eps=eps, scale=scale, round_qk=round_qk)
 
 
 @fused_decode_step.register_fake
-def _(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weight, A_log, dt_bias, eps=1e-6, scale=None):
+def _(x_qkv, z, a, b, conv_weight, conv_cache, state, norm_weight, A_log, dt_bias, eps=1e-6, scale=None,
+      round_qk=False):
     return z.new_empty(z.shape, dtype=x_qkv.dtype)
+
+
+@torch.library.custom_op(f"{NS}::serving_decode_step",
+                         mutates_args=("conv_live", "conv_commit", "state_live", "state_commit", "window", "win_len"))
+def serving_decode_step(mixed: Tensor, x_hidden: Tensor, slots: Tensor, conv_weight: Tensor, conv_live: Tensor,
+                        conv_commit: Tensor, state_live: Tensor, state_commit: Tensor, window: Tensor,
+                        win_len: Tensor, norm_weight: Tensor, A_log: Tensor, dt_bias: Tensor, eps: float = 1e-5,
+                        scale: Optional[float] = None, round_qk: bool = True) -> Tensor:
+    return ops.serving_decode_step(mixed, x_hidden, slots, conv_weight, conv_live, conv_commit, state_live,
+                                   state_commit, window, win_len, norm_weight, A_log, dt_bias, eps=eps, scale=scale,
+                                   round_qk=round_qk)
+
+
+@serving_decode_step.register_fake
+def _(mixed, x_hidden, slots, conv_weight, conv_live, conv_commit, state_live, state_commit, window, win_len,
+      norm_weight, A_log, dt_bias, eps=1e-5, scale=None, round_qk=True):
+    return mixed.new_empty(mixed.shape[0], state_live.shape[1], state_live.shape[3])
 
 
 # --------------------------------------------------------------------------------------------- row ops
@@ -153,5 +172,5 @@ def _(x, g, weight, eps=1e-5):
     return x.new_empty(x.shape), x.new_empty(x.shape[:-1], dtype=torch.float32)
 
 
-OPERATORS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "causal_conv1d", "l2norm",
-             "sigmoid", "gated_rmsnorm")
+OPERATORS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step",
+             "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
