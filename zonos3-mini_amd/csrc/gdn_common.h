@@ -91,6 +91,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+// x * sigmoid(x) with the hardware reciprocal (v_rcp_f32, ~1 ulp) in place of the division: a few
+// instructions instead of the division's ten; for results that are rounded to bf16 or compared at 1e-5.
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 }  // namespace zgdn
 

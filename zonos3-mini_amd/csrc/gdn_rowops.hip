@@ -1,12 +1,16 @@
 // Row-local operators of the GDN layer: depthwise causal conv1d (+ SiLU) with a rolling history over packed
 // sequences, q/k L2-norm, beta sigmoid and the gated RMSNorm of the output. All are HBM-streaming kernels:
 // consecutive threads own consecutive channels / elements, so every global access is coalesced.
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace zgdn {
 namespace {
 
-constexpr int CONV_CH = 64;       // tokens per conv workgroup (the chunk length of the chunk table)
+constexpr int CONV_CH = 64;       // tokens per chunk of the chunk table
+constexpr int CONV_TT = 16;       // tokens per conv workgroup
+constexpr int CONV_SPLIT = CONV_CH / CONV_TT;  // workgroups per chunk
 constexpr int CONV_THREADS = 256;
 constexpr int CONV_WMAX = 4;
 
@@ -16,90 +20,197 @@ __device__ __forceinline__ float rnd(float x) {
   else return x;
 }
 
-// y[t, c] = act(sum_j w[c, j] * x_{t - W + 1 + j}[c] + bias[c]) over the tokens of one chunk of one sequence,
-// with x_{<0} taken from the sequence's history (the last W-1 columns of its state row, oldest first) and
-// the new state row = the last SW raw inputs of [history | x]. The accumulation is fp32; like F.conv1d and
-// F.silu on `T` tensors, the conv result is rounded to T before the activation and the activation after.
+// CPT consecutive channels as loaded / stored by one thread (one 4-byte word for two bf16, a float2 for two
+// floats).
+__device__ __forceinline__ float as_float(float x) { return x; }
+__device__ __forceinline__ float as_float(bf16 x) { return bf16_to_f32(x.bits); }
+
+template <typename T, int CPT>
+struct chans;
+// ``raw`` is the loaded word(s), converted to floats by ``unpack`` where the values are used (so issuing a
+// load never waits for its data).
 template <typename T>
+struct chans<T, 1> {
+  using raw = T;
+  __device__ __forceinline__ static raw load(const T* p) { return *p; }
+  __device__ __forceinline__ static void unpack(raw w, float* v) { v[0] = as_float(w); }
+  __device__ __forceinline__ static void store(T* p, const float* v) { io<T>::store(p, v[0]); }
+};
+template <>
+struct chans<bf16, 2> {
+  using raw = uint32_t;
+  __device__ __forceinline__ static raw load(const bf16* p) { return *reinterpret_cast<const uint32_t*>(p); }
+  __device__ __forceinline__ static void unpack(raw w, float* v) {
+    v[0] = __uint_as_float(w << 16);
+    v[1] = __uint_as_float(w & 0xffff0000u);
+  }
+  __device__ __forceinline__ static void store(bf16* p, const float* v) {
+    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(v[0], v[1]);
+  }
+};
+template <>
+struct chans<float, 2> {
+  using raw = float2;
+  __device__ __forceinline__ static raw load(const float* p) { return *reinterpret_cast<const float2*>(p); }
+  __device__ __forceinline__ static void unpack(raw w, float* v) {
+    v[0] = w.x;
+    v[1] = w.y;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  }
+};
+
+// y[t, c] = act(sum_j w[c, j] * x_{t - W + 1 + j}[c] + bias[c]) over CONV_TT tokens of one chunk of one
+// sequence, CPT channels per thread, with x_{<0} taken from the sequence's history (the last W-1 columns of
+// its state row, oldest first); the first tile of a sequence also writes the new state row = the last SW raw
+// inputs of [history | x]. The accumulation is fp32; like F.conv1d and F.silu on `T` tensors, the conv
+// result is rounded to T before the activation and the activation after. A tile issues all its token loads
+// before the arithmetic, so its latency is one load round trip rather than one per token.
+template <typename T, int CPT, int WK>
 __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, const T* init, T* fin,
     T* __restrict__ y, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx, int n_seqs,
-    int n_chunks, int T_len, int D, int W, int SW, int act) {
-  const int c = blockIdx.y * CONV_THREADS + threadIdx.x;
-  if (c >= D) return;
+    int n_chunks, int T_len, int D, int W_arg, int SW, int act) {
+  const int W = WK > 0 ? WK : W_arg;  // WK: the width as a constant (the model's 4), 0: taken at run time
+  const int c0 = (blockIdx.y * CONV_THREADS + threadIdx.x) * CPT;
+  if (c0 >= D) return;
   int seq, j;
-  if (cu != nullptr && (int)blockIdx.x >= n_chunks) {
-    // trailing workgroups: empty packed sequences pass their state row through (zeros without one)
-    seq = blockIdx.x - n_chunks;
+  const int tile = blockIdx.x / CONV_SPLIT, sub = blockIdx.x % CONV_SPLIT;
+  if (cu != nullptr && (int)blockIdx.x >= n_chunks * CONV_SPLIT) {
+    // trailing workgroups, one per sequence: empty packed sequences pass their state row through (zeros
+    // without one)
+    seq = blockIdx.x - n_chunks * CONV_SPLIT;
     if (fin == nullptr || cu[seq + 1] != cu[seq]) return;
-    T* frow = fin + ((size_t)seq * D + c) * SW;
-    const T* hrow = init != nullptr ? init + ((size_t)seq * D + c) * SW : nullptr;
-    for (int i = 0; i < SW; ++i) io<T>::store(frow + i, hrow != nullptr ? io<T>::load(hrow + i) : 0.f);
+    for (int k = 0; k < CPT; ++k) {
+      T* frow = fin + ((size_t)seq * D + c0 + k) * SW;
+      const T* hrow = init != nullptr ? init + ((size_t)seq * D + c0 + k) * SW : nullptr;
+      for (int i = 0; i < SW; ++i) io<T>::store(frow + i, hrow != nullptr ? io<T>::load(hrow + i) : 0.f);
+    }
     return;
   }
   if (cu != nullptr) {
-    seq = chunk_idx[2 * blockIdx.x];
-    j = chunk_idx[2 * blockIdx.x + 1];
+    seq = chunk_idx[2 * tile];
+    j = chunk_idx[2 * tile + 1];
     if (seq < 0 || seq >= n_seqs || j < 0) return;
   } else {
     const int nt = max(1, (T_len + CONV_CH - 1) / CONV_CH);
-    seq = blockIdx.x / nt;
-    j = blockIdx.x % nt;
+    seq = tile / nt;
+    j = tile % nt;
   }
   const int bos = cu != nullptr ? cu[seq] : seq * T_len;
   const int len = cu != nullptr ? cu[seq + 1] - bos : T_len;
-  const int t0 = j * CONV_CH;
-  const int t1 = min(len, t0 + CONV_CH);
-  if (t0 >= len && len > 0) return;
+  const int t0 = j * CONV_CH + sub * CONV_TT;
+  const int t1 = min(len, t0 + CONV_TT);
+  const bool writes_state = fin != nullptr && j == 0 && sub == 0;
+  if (len == 0) {  // an empty sequence (a batch of T = 0) passes its state row through
+    if (writes_state)
+      for (int k = 0; k < CPT; ++k) {
+        T* frow = fin + ((size_t)seq * D + c0 + k) * SW;
+        const T* hrow = init != nullptr ? init + ((size_t)seq * D + c0 + k) * SW : nullptr;
+        for (int i = 0; i < SW; ++i) io<T>::store(frow + i, hrow != nullptr ? io<T>::load(hrow + i) : 0.f);
+      }
+    return;
+  }
+  if (t0 >= len) return;
 
-  float wc[CONV_WMAX], hist[CONV_WMAX];
+  // Every load below is unconditional (indices clamped into the sequence / state row, a missing state row
+  // replaced by x) and its value selected afterwards, so all of them issue back to back: a value written on
+  // one side of a branch and loaded on the other would make the compiler wait for each load in turn.
+  using C = chans<T, CPT>;
+  const int last = len - 1;
+  // Weights, bias, the tile's inputs and its history inside the sequence, all issued back to back with no
+  // condition (indices clamped into the sequence). Only a sequence's first tile needs the old state row
+  // (history before token 0) and the inputs of the new one; those loads come after, under conditions that
+  // are false for every other tile. Raw words are converted when used.
+  T wr[CPT][CONV_WMAX], br[CPT], hx[CPT][CONV_WMAX], hs[CPT][CONV_WMAX] = {}, nx[CPT][CONV_WMAX] = {},
+      ns[CPT][CONV_WMAX] = {};
+  typename C::raw xr[CONV_TT];
 #pragma unroll
-  for (int i = 0; i < CONV_WMAX; ++i) wc[i] = i < W ? io<T>::load(w + (size_t)c * W + i) : 0.f;
-  const float bc = bias != nullptr ? io<T>::load(bias + c) : 0.f;
-  const T* hrow = init != nullptr ? init + ((size_t)seq * D + c) * SW : nullptr;
-  // hist[i], i < W-1: the raw input W-1-i steps before token t0
+  for (int k = 0; k < CPT; ++k) {
+    const int c = c0 + k;
 #pragma unroll
-  for (int i = 0; i < CONV_WMAX - 1; ++i) {
-    float hv = 0.f;
-    if (i < W - 1) {
-      const int tt = t0 - (W - 1) + i;  // position within the sequence
-      if (tt >= 0) hv = io<T>::load(x + ((size_t)(bos + tt)) * D + c);
-      else if (hrow != nullptr) hv = io<T>::load(hrow + SW + tt);  // SW + tt >= SW - (W - 1) >= 0
-    }
-    hist[i] = hv;
+    for (int i = 0; i < CONV_WMAX; ++i) wr[k][i] = w[(size_t)c * W + min(i, W - 1)];
+    br[k] = (bias != nullptr ? bias : w)[bias != nullptr ? c : 0];
   }
-  for (int t = t0; t < t1; ++t) {
-    const float xv = io<T>::load(x + ((size_t)(bos + t)) * D + c);
-    float acc = bc;
 #pragma unroll
-    for (int i = 0; i < CONV_WMAX - 1; ++i)
-      if (i < W - 1) acc = fmaf(wc[i], hist[i], acc);
-    acc = fmaf(wc[W - 1], xv, acc);
-    float out = rnd<T>(acc);
-    if (act) out = rnd<T>(silu(out));
-    io<T>::store(y + ((size_t)(bos + t)) * D + c, out);
+  for (int i = 0; i < CONV_TT; ++i) xr[i] = C::load(x + ((size_t)(bos + min(t0 + i, last))) * D + c0);
 #pragma unroll
-    for (int i = 0; i < CONV_WMAX - 2; ++i)
-      if (i < W - 2) hist[i] = hist[i + 1];
-    if (W >= 2) hist[W - 2] = xv;
+  for (int k = 0; k < CPT; ++k) {
+    const T* xc = x + (size_t)bos * D + c0 + k;
+#pragma unroll
+    for (int i = 0; i < CONV_WMAX; ++i) hx[k][i] = xc[(size_t)min(max(t0 - (W - 1) + i, 0), last) * D];
   }
-  // the chunk holding the sequence start also writes the new state row (it alone reads the old one, so the
-  // state may be updated in place): the last SW raw inputs of [history | x], oldest first
-  if (fin != nullptr && j == 0) {
-    T* frow = fin + ((size_t)seq * D + c) * SW;
-    float nv[CONV_WMAX];
+  if (init != nullptr && (t0 < W - 1 || writes_state)) {
 #pragma unroll
-    for (int i = 0; i < CONV_WMAX; ++i) {
-      nv[i] = 0.f;
-      if (i < SW) {
-        const int tt = len - SW + i;  // position within the sequence (negative: from the old history)
-        if (tt >= 0) nv[i] = io<T>::load(x + ((size_t)(bos + tt)) * D + c);
-        else if (hrow != nullptr) nv[i] = io<T>::load(hrow + SW + tt);
+    for (int k = 0; k < CPT; ++k) {
+      const T* hrow = init + ((size_t)seq * D + c0 + k) * SW;
+#pragma unroll
+      for (int i = 0; i < CONV_WMAX; ++i) {
+        hs[k][i] = hrow[min(max(SW + t0 - (W - 1) + i, 0), SW - 1)];  // the input W-1-i steps before t0
+        ns[k][i] = hrow[min(max(SW + len - SW + i, 0), SW - 1)];      // the new row's i-th input
       }
     }
+  }
+  if (writes_state) {
 #pragma unroll
-    for (int i = 0; i < CONV_WMAX; ++i)
-      if (i < SW) io<T>::store(frow + i, nv[i]);
+    for (int k = 0; k < CPT; ++k) {
+      const T* xc = x + (size_t)bos * D + c0 + k;
+#pragma unroll
+      for (int i = 0; i < CONV_WMAX; ++i) nx[k][i] = xc[(size_t)min(max(len - SW + i, 0), last) * D];
+    }
+  }
+  // values used (a missing state row reads as zeros)
+  float wc[CPT][CONV_WMAX], hist[CPT][CONV_WMAX], nv[CPT][CONV_WMAX], bc[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    bc[k] = bias != nullptr ? as_float(br[k]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < CONV_WMAX; ++i) {
+      wc[k][i] = i < W ? as_float(wr[k][i]) : 0.f;
+      const int th = t0 - (W - 1) + i, tn = len - SW + i;
+      hist[k][i] = i >= W - 1 ? 0.f : th >= 0 ? as_float(hx[k][i]) : as_float(hs[k][i]);
+      nv[k][i] = tn >= 0 ? as_float(nx[k][i]) : as_float(ns[k][i]);
+    }
+  }
+  // full tiles (all but a sequence's last) run without a per-token guard
+  auto run = [&](auto full) {
+#pragma unroll
+    for (int i = 0; i < CONV_TT; ++i) {
+      if (!decltype(full)::value && t0 + i >= t1) continue;  // (not a break: the loop stays unrolled)
+      float xv[CPT], out[CPT];
+      C::unpack(xr[i], xv);
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        float acc = bc[k];
+#pragma unroll
+        for (int m = 0; m < CONV_WMAX - 1; ++m)
+          if (m < W - 1) acc = fmaf(wc[k][m], hist[k][m], acc);
+        acc = fmaf(wc[k][W - 1], xv[k], acc);
+        out[k] = rnd<T>(acc);
+        if (act) out[k] = rnd<T>(silu_fast(out[k]));
+#pragma unroll
+        for (int m = 0; m < CONV_WMAX - 2; ++m)
+          if (m < W - 2) hist[k][m] = hist[k][m + 1];
+        if (W >= 2) hist[k][W - 2] = xv[k];
+      }
+      chans<T, CPT>::store(y + ((size_t)(bos + t0 + i)) * D + c0, out);
+    }
+  };
+  if (t1 - t0 == CONV_TT)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+  // the tile holding the sequence start writes the new state row (it alone reads the old one, so the state
+  // may be updated in place)
+  if (writes_state) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      T* frow = fin + ((size_t)seq * D + c0 + k) * SW;
+#pragma unroll
+      for (int i = 0; i < CONV_WMAX; ++i)
+        if (i < SW) io<T>::store(frow + i, nv[k][i]);
+    }
   }
 }
 
@@ -183,23 +294,34 @@ extern "C" int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const v
   if (cu_seqlens != nullptr) {
     if (B != 1 || chunk_indices == nullptr || n_seqs < 1 || n_chunks < 0)
       return fail(ZGDN_EINVAL, "%s: packed sequences need B == 1, chunk_indices and n_seqs >= 1", fn);
-    grid_x = n_chunks + n_seqs;  // + one workgroup column per sequence for empty ones
+    grid_x = n_chunks * CONV_SPLIT + n_seqs;  // + one workgroup column per sequence for empty ones
   } else {
     n_seqs = B;
-    grid_x = B * ((T + CONV_CH - 1) / CONV_CH);
-    if (T == 0) grid_x = B;  // empty sequences still pass their state through
+    grid_x = B * ((T + CONV_CH - 1) / CONV_CH) * CONV_SPLIT;
+    if (T == 0) grid_x = B * CONV_SPLIT;  // empty sequences still pass their state through
   }
   if (grid_x == 0) return check_launch(fn);
-  dim3 grid(grid_x, (D + CONV_THREADS - 1) / CONV_THREADS);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == ZGDN_F32)
-    hipLaunchKernelGGL(conv_kernel<float>, grid, dim3(CONV_THREADS), 0, s, (const float*)x, (const float*)weight,
-                       (const float*)bias, (const float*)initial_state, (float*)final_state, (float*)y, cu_seqlens,
-                       chunk_indices, n_seqs, n_chunks, T, D, W, state_width, activation);
-  else
-    hipLaunchKernelGGL(conv_kernel<bf16>, grid, dim3(CONV_THREADS), 0, s, (const bf16*)x, (const bf16*)weight,
-                       (const bf16*)bias, (const bf16*)initial_state, (bf16*)final_state, (bf16*)y, cu_seqlens,
-                       chunk_indices, n_seqs, n_chunks, T, D, W, state_width, activation);
+  auto go = [&](auto* tag, auto cpt) {
+    using TT = std::remove_pointer_t<decltype(tag)>;
+    constexpr int CPT = decltype(cpt)::value;
+    const int per_wg = CONV_THREADS * CPT;
+    dim3 grid(grid_x, (D + per_wg - 1) / per_wg);
+    auto kernel = W == 4 ? conv_kernel<TT, CPT, 4> : conv_kernel<TT, CPT, 0>;
+    hipLaunchKernelGGL(kernel, grid, dim3(CONV_THREADS), 0, s, (const TT*)x, (const TT*)weight, (const TT*)bias,
+                       (const TT*)initial_state, (TT*)final_state, (TT*)y, cu_seqlens, chunk_indices, n_seqs,
+                       n_chunks, T, D, W, state_width, activation);
+  };
+  using One = std::integral_constant<int, 1>;
+  using Two = std::integral_constant<int, 2>;
+  const bool pairs = D % 2 == 0;  // two channels per thread keep each pair 4- or 8-byte aligned
+  if (dtype == ZGDN_F32) {
+    if (pairs) go((float*)nullptr, Two{});
+    else go((float*)nullptr, One{});
+  } else {
+    if (pairs) go((bf16*)nullptr, Two{});
+    else go((bf16*)nullptr, One{});
+  }
   return check_launch(fn);
 }
 
