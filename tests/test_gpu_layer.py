@@ -149,3 +149,40 @@ def test_seam_refuses_what_it_does_not_compute(gdn, cuda):
         fla.layer_norm_gated_fwd(t[0, 0], t[0, 0], t[0, 0, 0], bias=t[0, 0, 0])
     with pytest.raises(RuntimeError, match="residual"):
         fla.causal_conv1d_fwd(t[0], t[0, 0, :, :4].T.contiguous(), residual=t[0])
+
+
+def test_layer_with_weights_read_from_gguf(gdn, cuda, tmp_path):
+    """A layer's weights stored under the GGUF GDN names (in_proj as Q8_0 blocks, wo as F16, the rest F32),
+    read back by formats.read_gguf / gdn_layer_weights and run through the drop-in: against the oracle given
+    the same (dequantised) weights, a 70-row prefill then a decode row."""
+    from gdn_testing import q8_0, write_gguf
+
+    announce("layer drop-in with GGUF-read weights, prefill 70 + 1 decode, bf16")
+    formats = importlib.import_module("zonos3-mini_amd.formats")
+    layer = importlib.import_module("zonos3-mini_amd.layer")
+    w = _weights(4301, torch.float32)
+    np = __import__("numpy")
+    tensors = {
+        "blk.0.gdn_in.weight": (8, q8_0(w["in_proj"].numpy()), tuple(w["in_proj"].shape)),
+        "blk.0.gdn_norm.weight": (0, w["out_weight"].numpy().tobytes(), (128,)),
+        "blk.0.gdn_A_log": (0, w["A_log"].numpy().tobytes(), (HEADS,)),
+        "blk.0.gdn_dt_bias": (0, w["dt_bias"].numpy().tobytes(), (HEADS,)),
+        "blk.0.gdn_conv.weight": (0, w["conv"][:, 0].contiguous().numpy().tobytes(), (3 * HEADS * HD, 4)),
+        "blk.0.attn_output.weight": (1, w["wo"].numpy().astype(np.float16).tobytes(), tuple(w["wo"].shape)),
+    }
+    write_gguf(tmp_path / "gdn.gguf", {"gdn.head_count": HEADS, "gdn.head_dim": HD, "gdn.conv_kernel": 4}, tensors)
+    _, t = formats.read_gguf(tmp_path / "gdn.gguf")
+    read = {k: v.to(torch.bfloat16) if k not in ("A_log", "dt_bias") else v
+            for k, v in formats.gdn_layer_weights(t, 0).items()}
+    assert (read["in_proj"].float() - w["in_proj"]).abs().max() < 0.05 * w["in_proj"].abs().max()  # Q8_0 grid
+    model = _Model(read, cuda)
+    layer.patch(model)
+    x = torch.randn(71, DIM, generator=torch.Generator().manual_seed(4302)).to(torch.bfloat16)
+    cache = _Cache()
+    conv_ref, state_ref = None, None
+    for lo, hi in ((0, 70), (70, 71)):
+        y = model._gdn(x[lo:hi].to(cuda), 0, cache)
+        torch.cuda.synchronize()
+        y_ref, conv_ref, state_ref, _ = O.gdn_layer(x[lo:hi], read, conv_ref, state_ref, heads=HEADS, head_dim=HD)
+        assert rel_err(y.cpu(), y_ref) < 2e-2, (lo, rel_err(y.cpu(), y_ref))
+        assert rel_err(cache.gdn_state[0].cpu(), state_ref) < 1e-3, lo
