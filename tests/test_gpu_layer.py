@@ -8,6 +8,7 @@ import importlib
 from dataclasses import dataclass, field
 from types import SimpleNamespace
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -161,7 +162,6 @@ def test_layer_with_weights_read_from_gguf(gdn, cuda, tmp_path):
     formats = importlib.import_module("zonos3-mini_amd.formats")
     layer = importlib.import_module("zonos3-mini_amd.layer")
     w = _weights(4301, torch.float32)
-    np = __import__("numpy")
     tensors = {
         "blk.0.gdn_in.weight": (8, q8_0(w["in_proj"].numpy()), tuple(w["in_proj"].shape)),
         "blk.0.gdn_norm.weight": (0, w["out_weight"].numpy().tobytes(), (128,)),
