@@ -50,7 +50,7 @@ def _args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres"], default=None,
                    help="run one workload only (profiling runs); the JSON line then carries that workload")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
@@ -269,6 +269,28 @@ def bench_fused(torch, gdn, steps_per_graph=16):
     }
 
 
+ATTNRES = dict(S=23, T=4096, D=1024)  # the release LM's final mix: embedding + 2 x 11 sublayer outputs
+
+
+def bench_attnres(torch, gdn):
+    """Residual routing (full_attnres_route, lm.py:384-389) over 23 sources of 4096 tokens x 1024, bf16:
+    every source row read once, the mix written once."""
+    dev = torch.device("cuda:0")
+    c = ATTNRES
+    g = torch.Generator(device=dev).manual_seed(1007)
+    srcs = [torch.randn(c["T"], c["D"], generator=g, device=dev).to(torch.bfloat16) for _ in range(c["S"])]
+    q = (0.3 * torch.randn(c["D"], generator=g, device=dev)).to(torch.bfloat16)
+    stream = torch.cuda.Stream(dev)
+    k_ms = kernel_ms(torch, stream, lambda: gdn.ops.attnres_route(srcs, q, 1e-5), 50)
+    nbytes = (c["S"] + 1) * c["T"] * c["D"] * 2
+    achieved = nbytes / (k_ms * 1e-3) / 1e9
+    return {"workload": "full_attnres_route: 23 sources x 4096 tokens x 1024, bf16 (the release LM's final mix)",
+            "tokens_per_s": round(c["T"] / (k_ms * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "attnres_kernel<bf16,2>",
+                         "kernel_us": round(k_ms * 1e3, 3), "algorithmic_bytes": nbytes}}
+
+
 SERVING = dict(hidden=1024, prompt=100, batch_sizes=(2, 32))
 
 
@@ -425,6 +447,9 @@ def main():
     if a.only == "serving":
         print(json.dumps({"workload_only": a.only, **bench_serving(torch)}), flush=True)
         return
+    if a.only == "attnres":
+        print(json.dumps({"workload_only": a.only, **bench_attnres(torch, gdn)}), flush=True)
+        return
     dec = bench_decode(torch, gdn, a.steps, a.warmup)
     line = {
         "metric": METRIC,
@@ -463,6 +488,7 @@ def main():
     line["varlen_prefill"] = bench_varlen(torch, gdn)
     line["fused_decode_block"] = bench_fused(torch, gdn)
     line["serving_decode"] = bench_serving(torch)
+    line["attnres_route"] = bench_attnres(torch, gdn)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
         line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)

@@ -122,6 +122,18 @@ int zgdn_serving_decode_step(const void* mixed, long mixed_ld, const void* x_hid
                              float eps, float scale, int qk_round, void* stream);
 
 /*
+ * Full Attention-Residual routing of the LM's residual bank: out = sum_s softmax_s(rms_norm(x_s) . query) x_s
+ * per token, the logits and softmax in fp32. Replaces full_attnres_route of
+ * model/src/zonos3/reference/lm.py:384-389 (a list of sources) and of
+ * servers/sgl/src/zonos3_sgl/models/zonos3.py:99-113 (a stacked [S, T, dim] bank), without stacking.
+ *   sources: host array of n_sources (1..64) device pointers, each to `tokens` rows of `dim` elements spaced
+ *   row_stride elements apart (dim a multiple of 8, <= 2048); query [dim]; out [tokens, dim] contiguous; all of
+ *   element type `dtype`. eps: the rms_norm eps.
+ */
+int zgdn_attnres_route(const void* const* sources, int n_sources, int tokens, int dim, long row_stride, int dtype,
+                       const void* query, float eps, void* out, void* stream);
+
+/*
  * Depthwise causal conv1d over packed sequences with a rolling history, optional SiLU. Replaces FLA's
  * causal_conv1d_fwd as called at servers/sgl/src/zonos3_sgl/models/gdn.py:403-414, and the conv of
  * model/src/zonos3/reference/lm.py:563-568 (cross-correlation, weight tap 0 oldest).

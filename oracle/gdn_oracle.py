@@ -15,6 +15,11 @@ Two independent statements of the same mathematics live here:
   Agreement between the loop and the chunked form is a mathematical identity, and the tests use it to pin
   both.
 
+The residual routing that feeds and consumes each GDN layer (``attnres_route``, ``lm.py:384-389``) has a
+torch restatement and a float64 one (``attnres_route_np``); its pins are closed forms (one source returns
+it, a zero query averages the sources, a dominant logit selects its source, order of sources is
+irrelevant) and the float64 statement.
+
 Conventions (all from the reference):
   q, k   [.., T, Hk, K]       v [.., T, Hv, V]       g (log decay), beta [.., T, Hv]
   state  [N, Hv, V, K] float32, value-major (FLA ``state_v_first=True``; lm.py:577, gdn.py:427)
@@ -227,6 +232,29 @@ def fused_decode_step(x_qkv, z, a, b, conv_w, conv_cache, state, norm_w, A_log, 
         caches.append(hist)
         states.append(s)
     return torch.stack(outs), torch.stack(caches), torch.stack(states)
+
+
+def attnres_route(sources, query, eps):
+    """Full Attention-Residual routing, ``lm.py:384-389`` (same ops, same casts): the sources stacked, keys =
+    weightless rms_norm of each source, logits = sum(keys * query) in float32, softmax over the sources cast
+    back to the sources' dtype, the weighted sum of the raw sources. sources: a list of [T, dim] tensors or a
+    [S, T, dim] tensor."""
+    bank = torch.stack(list(sources)) if not torch.is_tensor(sources) else sources
+    keys = F.rms_norm(bank, (bank.shape[-1],), eps=eps)
+    scores = (keys * query).sum(-1, dtype=torch.float32)
+    weights = scores.softmax(0).to(bank.dtype)
+    return (bank * weights.unsqueeze(-1)).sum(0)
+
+
+def attnres_route_np(sources, query, eps) -> np.ndarray:
+    """The same equation in float64 with no intermediate rounding (an independent statement)."""
+    bank = np.stack([_f64(s) for s in sources])
+    q = _f64(query)
+    keys = bank / np.sqrt((bank**2).mean(-1, keepdims=True) + eps)
+    logits = (keys * q).sum(-1)
+    w = np.exp(logits - logits.max(0, keepdims=True))
+    w /= w.sum(0, keepdims=True)
+    return (bank * w[..., None]).sum(0)
 
 
 # ---------------------------------------------------------------------------- float64 statements (numpy)

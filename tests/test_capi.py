@@ -23,7 +23,7 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
-            "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step"} == _declared()
+            "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -98,6 +98,14 @@ def test_bad_arguments_fail_with_a_message(gdn):
     assert lib.zgdn_serving_decode_step(*serve) == native.EUNSUPPORTED and b"Hv/Hk=8" in lib.zgdn_last_error()
     serve[9], serve[6] = 4, 0
     assert lib.zgdn_serving_decode_step(*serve) == native.EINVAL and b"n_slots=0" in lib.zgdn_last_error()
+    srcs = (ctypes.c_void_p * 2)(16, 16)
+    assert lib.zgdn_attnres_route(srcs, 65, 4, 1024, 1024, 1, p, 1e-5, p, None) == native.EUNSUPPORTED
+    assert lib.zgdn_attnres_route(srcs, 2, 4, 1028, 1028, 1, p, 1e-5, p, None) == native.EUNSUPPORTED
+    assert b"multiple of 8" in lib.zgdn_last_error()
+    assert lib.zgdn_attnres_route(srcs, 2, 4, 1024, 1000, 1, p, 1e-5, p, None) == native.EINVAL
+    srcs[1] = None
+    assert lib.zgdn_attnres_route(srcs, 2, 4, 1024, 1024, 1, p, 1e-5, p, None) == native.EINVAL
+    assert b"null source 1" in lib.zgdn_last_error()
 
 
 def test_host_validation_refuses_cpu_tensors(gdn):

@@ -295,3 +295,26 @@ def _pins_pass(fn) -> bool:
 def test_planted_mistakes_are_caught(kind):
     assert _pins_pass(O.gated_delta_sequence)
     assert not _pins_pass(_mutant(kind))
+
+
+# ------------------------------------------------------------------------------ residual routing (lm.py:384)
+
+
+def test_attnres_route_closed_forms():
+    gen = torch.Generator().manual_seed(91)
+    srcs = [torch.randn(5, 64, generator=gen) for _ in range(4)]
+    q = torch.randn(64, generator=gen)
+    # one source: softmax over one logit is 1
+    assert torch.allclose(O.attnres_route(srcs[:1], q, 1e-5), srcs[0], atol=1e-6)
+    # zero query: equal weights, the mean of the sources
+    assert torch.allclose(O.attnres_route(srcs, torch.zeros(64), 1e-5), torch.stack(srcs).mean(0), atol=1e-6)
+    # a query along one source's direction of one token, scaled up: that source wins for that token
+    big = 200.0 * srcs[2][3] / srcs[2][3].norm()
+    assert torch.allclose(O.attnres_route(srcs, big, 1e-5)[3], srcs[2][3], atol=1e-4)
+    # the order of the sources does not matter
+    perm = [srcs[i] for i in (2, 0, 3, 1)]
+    assert torch.allclose(O.attnres_route(srcs, q, 1e-5), O.attnres_route(perm, q, 1e-5), atol=1e-6)
+    # torch restatement == float64 statement (fp32 inputs)
+    assert rel_err(O.attnres_route(srcs, q, 1e-5), O.attnres_route_np(srcs, q, 1e-5)) < 1e-6
+    # a stacked bank is the same as the list
+    assert torch.equal(O.attnres_route(torch.stack(srcs), q, 1e-5), O.attnres_route(srcs, q, 1e-5))

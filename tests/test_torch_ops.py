@@ -10,8 +10,8 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 from gdn_testing import announce
 from oracle import gdn_oracle as O
 
-OPS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step", "causal_conv1d",
-       "l2norm", "sigmoid", "gated_rmsnorm")
+OPS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step", "attnres_route",
+       "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
 
 
 def test_registered_with_mutation_annotations(gdn):
@@ -62,6 +62,9 @@ def test_fake_shapes(gdn):
                                   torch.empty(1536, 4, dtype=torch.bfloat16), conv4, conv4, st5, st5, win,
                                   torch.empty(5, dtype=torch.int32), nw, hv, hv)
         assert y.shape == (3, 4, 128) and y.dtype == torch.bfloat16
+        bank = [torch.empty(9, 1024, dtype=torch.bfloat16) for _ in range(5)]
+        r = z.attnres_route(bank, torch.empty(1024, dtype=torch.bfloat16), 1e-5)
+        assert r.shape == (9, 1024) and r.dtype == torch.bfloat16
         xc = torch.empty(1, 130, 96)
         y, fin = z.causal_conv1d(xc, torch.empty(96, 4), None, None, cu, None, "silu", 3)
         assert y.shape == xc.shape and fin.shape == (3, 96, 3)

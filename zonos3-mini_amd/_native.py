@@ -46,6 +46,10 @@ SIGNATURES: dict[str, tuple] = {
         [_P, c_long, _P, c_int, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          _P, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_float, c_float, c_int, _P],
     ),
+    "zgdn_attnres_route": (
+        c_int,
+        [POINTER(c_void_p), c_int, c_int, c_int, c_long, c_int, _P, c_float, _P, _P],
+    ),
     "zgdn_causal_conv1d_fwd": (
         c_int,
         [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P],

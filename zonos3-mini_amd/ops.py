@@ -8,6 +8,8 @@ without synchronising the host, so every call can be captured into a HIP graph. 
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native
@@ -302,6 +304,42 @@ def serving_decode_step(mixed, x_hidden, slots, conv_weight, conv_live, conv_com
         window.data_ptr(), win_len.data_ptr(), window.shape[1], A_log.data_ptr(), dt_bias.data_ptr(),
         norm_weight.data_ptr(), out.data_ptr(), float(eps), scale, int(bool(round_qk)), _stream(dev),
     )
+    return out
+
+
+def attnres_route(sources, query, eps):
+    """Full Attention-Residual routing (lm.py:384-389): per token, softmax over the sources of
+    rms_norm(x_s) . query (fp32), then the weighted sum of the raw sources.
+
+    sources: a list of [T, dim] tensors (lm.py) or one [S, T, dim] bank (the serving layer, zonos3.py:99-113),
+    read in place (no stacking); query [dim]; one dtype (float32 / bfloat16). Returns [T, dim]."""
+    if torch.is_tensor(sources):
+        _require(sources.dim() == 3, f"sources: expected [S, T, dim], got {tuple(sources.shape)}")
+        sources = list(sources.unbind(0))
+    _require(len(sources) >= 1, "sources: at least one source")
+    first = sources[0]
+    _require(isinstance(first, torch.Tensor) and first.is_cuda,
+             "sources[0]: must be a GPU tensor; there is no CPU path")
+    dev = first.device
+    _require(first.dim() == 2, f"sources: expected [T, dim] rows, got {tuple(first.shape)}")
+    T, D = first.shape
+    rows = []
+    for i, s in enumerate(sources):  # rows may be strided (a bank's slices, a wider tensor's columns)
+        _require(isinstance(s, torch.Tensor) and s.device == dev, f"sources[{i}]: expected a tensor on {dev}")
+        _require(s.shape == first.shape and s.dtype == first.dtype,
+                 f"sources[{i}]: {tuple(s.shape)} {s.dtype}, expected {tuple(first.shape)} {first.dtype}")
+        rows.append(s)
+    stride = first.stride(0) if T > 1 else D
+    if any(s.stride(1) != 1 or (T > 1 and s.stride(0) != stride) for s in rows):
+        rows = [s.contiguous() for s in rows]
+        stride = D
+    _on_gpu("query", query, dev)
+    _require(query.shape == (D,) and query.dtype == first.dtype and query.is_contiguous(),
+             f"query: expected contiguous [{D}] {first.dtype}")
+    out = torch.empty(T, D, device=dev, dtype=first.dtype)
+    ptrs = (ctypes.c_void_p * len(rows))(*[s.data_ptr() for s in rows])
+    _native.call("zgdn_attnres_route", ptrs, len(rows), T, D, stride, _code(first, "sources"), query.data_ptr(),
+                 float(eps), out.data_ptr(), _stream(dev))
     return out
 
 

@@ -13,6 +13,7 @@ state in place declare it in ``mutates_args``.
 | ``zgdn::chunk_fwd`` | FLA ``chunk_gated_delta_rule_fwd`` (gdn.py:418-434) |
 | ``zgdn::fused_decode_step`` | lm.py:563-587 for one new row per stream, conv cache and state in place |
 | ``zgdn::serving_decode_step`` | the serving layer's static decode (gdn.py:329-355) on per-slot caches in place |
+| ``zgdn::attnres_route`` | ``full_attnres_route`` (lm.py:384-389; zonos3.py:99-113) |
 | ``zgdn::causal_conv1d`` | FLA ``causal_conv1d_fwd`` (gdn.py:403-414); lm.py:563-568 |
 | ``zgdn::l2norm`` | FLA ``l2norm_fwd`` (gdn.py:416-417); lm.py:570-571 |
 | ``zgdn::sigmoid`` | FLA ``fused_beta_sigmoid_fwd`` (gdn.py:423); lm.py:573 |
@@ -22,7 +23,7 @@ state in place declare it in ``mutates_args``.
 from __future__ import annotations
 
 import importlib
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 from torch import Tensor
@@ -122,6 +123,16 @@ def _(mixed, x_hidden, slots, conv_weight, conv_live, conv_commit, state_live, s
     return mixed.new_empty(mixed.shape[0], state_live.shape[1], state_live.shape[3])
 
 
+@torch.library.custom_op(f"{NS}::attnres_route", mutates_args=())
+def attnres_route(sources: List[Tensor], query: Tensor, eps: float) -> Tensor:
+    return ops.attnres_route(sources, query, eps)
+
+
+@attnres_route.register_fake
+def _(sources, query, eps):
+    return sources[0].new_empty(sources[0].shape)
+
+
 # --------------------------------------------------------------------------------------------- row ops
 
 
@@ -173,4 +184,4 @@ def _(x, g, weight, eps=1e-5):
 
 
 OPERATORS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step",
-             "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
+             "attnres_route", "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
