@@ -298,6 +298,10 @@ __global__ __launch_bounds__(64 * STEP_NWAVES) void step_kernel(
   const int last = n_tiles - 1;
   Tile b0, b1;
   load(ti, b0);
+  if (stride >= n_tiles) {  // one item per wave: nothing to prefetch
+    process(ti, b0);
+    return;
+  }
   for (;;) {  // two buffers in turn; every wave leaves after its last tile
     const int t1 = ti + stride;
     load(min(t1, last), b1);
@@ -351,7 +355,11 @@ bool launch_step(const RecArgs& a, hipStream_t stream) {
   if (!tiled && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * STEP_NWAVES, 0) != hipSuccess ||
                  per_cu < 1))
     per_cu = 4;
-  const long long wgs = std::min<long long>((n_tiles + STEP_NWAVES - 1) / STEP_NWAVES, (long long)per_cu * n_cu);
+  const long long all = (n_tiles + STEP_NWAVES - 1) / STEP_NWAVES;  // one item per wave
+  long long wgs = std::min<long long>(all, (long long)per_cu * n_cu);
+  // single groups: up to two per resident wave would leave some waves one behind the others for a whole
+  // group's latency; one group per wave (the hardware queues the rest) finishes sooner there (B=16, H=16)
+  if (!tiled && all <= 2LL * per_cu * n_cu) wgs = all;
   hipLaunchKernelGGL(kernel, dim3((unsigned)wgs), dim3(64 * STEP_NWAVES), 0, stream, (const TIn*)a.q,
                      (const TIn*)a.k, (const TIn*)a.v, (const TG*)a.g, (const TG*)a.beta, a.A_log, a.dt_bias,
                      a.qk_l2norm, a.s_in, a.s_out, (TOut*)a.o, (int)n_tiles, a.Hk, a.Hv, a.V, a.scale);
