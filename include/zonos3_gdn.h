@@ -6,7 +6,8 @@
  * therefore capturable into a HIP graph. Return value: ZGDN_OK, or an error code with a message available
  * from zgdn_last_error() (per calling thread).
  *
- * Layouts (all contiguous, row-major, the reference's FLA calling convention):
+ * Layouts (row-major, the reference's FLA calling convention; contiguous except where an entry point takes
+ * row strides):
  *   q, k          [B, T, Hk, K]     v, o  [B, T, Hv, V]     g (log decay), beta  [B, T, Hv]
  *   state         [N, Hv, V, K] float32, value-major ("state_v_first"); N = B, or the number of packed
  *                 sequences when cu_seqlens [N+1] (int32) is given with B == 1.
@@ -63,10 +64,14 @@ size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
  * accumulation: the prefill core. Replaces FLA's chunk_gated_delta_rule_fwd as called at
  * servers/sgl/src/zonos3_sgl/models/gdn.py:418-434 (state_v_first=True, chunk_size=64, output o and the
  * final state), itself the chunked form of model/src/zonos3/reference/lm.py:574-583.
- *   q, k, v: bf16, K == V == 128. o: bf16 [B, T, Hv, V].
- *   g, beta: gb_dtype. With A_log and dt_bias (float32 [Hv], both or neither) g holds the raw gate input a
- *   and the log decay is -exp(A_log[h]) * softplus(a + dt_bias[h]) (FLA use_gate_in_kernel=True,
- *   gdn.py:430-432); otherwise g is the log decay.
+ *   q, k, v: bf16, K == V == 128, rows of [B * T] tokens q_ld / k_ld / v_ld elements apart (a token's heads
+ *   contiguous; a multiple of 8 elements, bases 16-byte aligned), so that q, k, v may be column slices of one
+ *   wider row such as the conv output. o: bf16 [B, T, Hv, V] (dense).
+ *   g, beta: gb_dtype, rows of Hv values gb_ld elements apart (column slices of the input projection read in
+ *   place). With A_log and dt_bias (float32 [Hv], both or neither) g holds the raw gate input a and the log
+ *   decay is -exp(A_log[h]) * softplus(a + dt_bias[h]) (FLA use_gate_in_kernel=True, gdn.py:430-432);
+ *   otherwise g is the log decay. beta_sigmoid != 0: beta holds the raw input b and the kernel uses
+ *   sigmoid(b) (fp32), the value zgdn_sigmoid_fwd would give (FLA fused_beta_sigmoid_fwd, gdn.py:423).
  *   qk_l2norm != 0: q and k are the raw rows and are L2-normalised in the kernel (fp32 factors; the
  *   normalised rows are never rounded to bf16), as lm.py:570-571 does before its fp32 recurrence.
  *   cu_seqlens [n_seqs+1] + chunk_indices [n_chunks, 2] (sequence, chunk within it; the table of
@@ -78,7 +83,8 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
                    int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
                    const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
                    const int32_t* chunk_indices, int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K,
-                   int V, float scale, void* workspace, size_t workspace_bytes, void* stream);
+                   int V, long q_ld, long k_ld, long v_ld, long gb_ld, int beta_sigmoid, float scale,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * One single-token step of the whole GDN block for B independent streams, fused in one launch: depthwise
@@ -138,7 +144,8 @@ int zgdn_attnres_route(const void* const* sources, int n_sources, int tokens, in
  * causal_conv1d_fwd as called at servers/sgl/src/zonos3_sgl/models/gdn.py:403-414, and the conv of
  * model/src/zonos3/reference/lm.py:563-568 (cross-correlation, weight tap 0 oldest).
  *   x, y [B, T, D] (packed: B == 1 with cu_seqlens [n_seqs+1] and chunk_indices [n_chunks, 2] of 64-token
- *   chunks); weight [D, W], bias [D] or NULL; all of element type `dtype`; W <= 4.
+ *   chunks); the rows of x are x_ld >= D elements apart (the q|k|v columns of the input projection are read in
+ *   place), y is dense; weight [D, W], bias [D] or NULL; all of element type `dtype`; W <= 4.
  *   State rows [n_seqs, D, state_width], state_width in [W-1, 4]: the raw inputs before the sequence, oldest
  *   first (the last W-1 columns are the taps' history). lm.py keeps [D, W-1] (state_width W-1); the serving
  *   layer keeps [N, D, W] (state_width W). final_state receives the last state_width raw inputs of
@@ -150,14 +157,17 @@ int zgdn_attnres_route(const void* const* sources, int n_sources, int tokens, in
 int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, int dtype,
                            const void* initial_state, void* final_state, int state_width, void* y,
                            const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
-                           int B, int T, int D, int W, int activation, void* stream);
+                           int B, int T, int D, int W, int activation, long x_ld, void* stream);
 
 /*
  * Row-wise L2 norm y = x * rsqrt(sum x^2 + eps), D <= 1024; rstd [rows] (float32) receives the factor when
  * not NULL. Replaces FLA's l2norm_fwd (gdn.py:416-417) and lm.py:570-571 (eps 1e-6).
+ *   y: dense [rows, D]. Row r of x starts at x + (r / x_group) * x_ld + (r % x_group) * D, so a token's
+ *   x_group heads may sit inside a wider row (q or k of the conv output, read in place); dense x: x_group 1,
+ *   x_ld D.
  */
-int zgdn_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd, int rows, int D, float eps,
-                    void* stream);
+int zgdn_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd, int rows, int D, int x_group,
+                    long x_ld, float eps, void* stream);
 
 /*
  * y = sigmoid(x) * scale elementwise. Replaces FLA's fused_beta_sigmoid_fwd (gdn.py:423) and the beta of
@@ -169,9 +179,12 @@ int zgdn_sigmoid_fwd(const void* x, int x_dtype, void* y, int y_dtype, size_t n,
  * Gated RMSNorm of the recurrent output, y = (rms_norm(x) * weight).to(dtype) * silu(g), product in fp32 then
  * cast, one row of D <= 1024 at a time; rstd [rows] receives 1/rms when not NULL. Replaces FLA's
  * layer_norm_gated_fwd(activation="swish", is_rms_norm=True) at gdn.py:435-445 and lm.py:584-587.
+ *   x, y: dense [rows, D]. Row r's gate starts at g + (r / g_group) * g_ld + (r % g_group) * D, so a token's
+ *   g_group per-head gates may sit inside a wider row (z of the input projection, read in place); dense g:
+ *   g_group 1, g_ld D.
  */
 int zgdn_gated_rmsnorm_fwd(const void* x, const void* g, const void* weight, int dtype, void* y, float* rstd,
-                           int rows, int D, float eps, void* stream);
+                           int rows, int D, int g_group, long g_ld, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(gdn):
     for name in _declared():
         assert hasattr(lib, name), name
     assert set(native.SIGNATURES) == _declared()
-    assert lib.zgdn_abi_version() == 1
+    assert lib.zgdn_abi_version() == native.ABI_VERSION == 2
 
 
 def _rec_args(**over):
@@ -67,21 +67,32 @@ def test_bad_arguments_fail_with_a_message(gdn):
     with pytest.raises(RuntimeError, match="null"):
         native.call("zgdn_recurrent_fwd", *_rec_args(q=None))
     # chunked prefill: head size, dtype and workspace checks
-    chunk = [p, p, p, 1, p, p, 0, None, None, 0, None, None, p, None, None, 1, 0, 1, 64, 1, 1, 128, 128, 1.0, p, 0,
-             None]
+    chunk = [p, p, p, 1, p, p, 0, None, None, 0, None, None, p, None, None, 1, 0, 1, 64, 1, 1, 128, 128,
+             128, 128, 128, 1, 0, 1.0, p, 0, None]
     assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"workspace" in lib.zgdn_last_error()
+    chunk[23] = 1536 + 4  # q row stride not a multiple of 8 elements
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"row strides" in lib.zgdn_last_error()
+    chunk[23], chunk[26] = 128, 0  # g/beta rows narrower than the heads
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"row strides" in lib.zgdn_last_error()
+    chunk[26] = 1
     chunk[21] = 64  # K
     assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=64" in lib.zgdn_last_error()
     chunk[21], chunk[3] = 128, 0  # fp32 q/k/v
     assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"bf16" in lib.zgdn_last_error()
     assert lib.zgdn_chunk_workspace_size(64, 16) == 64 * 16 * 98560
     # conv width, state width; row-op sizes; fused block group size
-    conv = [p, p, None, 1, None, None, 4, p, None, None, 1, 0, 1, 8, 16, 5, 1, None]
+    conv = [p, p, None, 1, None, None, 4, p, None, None, 1, 0, 1, 8, 16, 5, 1, 16, None]
     assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EUNSUPPORTED and b"width 5" in lib.zgdn_last_error()
     conv[15], conv[6] = 4, 2
     assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EINVAL and b"state width" in lib.zgdn_last_error()
-    assert lib.zgdn_l2norm_fwd(p, 1, p, 1, None, 4, 2048, 1e-6, None) == native.EUNSUPPORTED
-    assert lib.zgdn_gated_rmsnorm_fwd(p, None, p, 1, p, None, 4, 128, 1e-5, None) == native.EINVAL
+    conv[6], conv[17] = 4, 8
+    assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EINVAL and b"row stride" in lib.zgdn_last_error()
+    assert lib.zgdn_l2norm_fwd(p, 1, p, 1, None, 4, 2048, 1, 2048, 1e-6, None) == native.EUNSUPPORTED
+    assert lib.zgdn_l2norm_fwd(p, 1, p, 1, None, 8, 128, 4, 256, 1e-6, None) == native.EINVAL
+    assert b"x rows" in lib.zgdn_last_error()
+    assert lib.zgdn_gated_rmsnorm_fwd(p, None, p, 1, p, None, 4, 128, 1, 128, 1e-5, None) == native.EINVAL
+    assert lib.zgdn_gated_rmsnorm_fwd(p, p, p, 1, p, None, 4, 128, 4, 500, 1e-5, None) == native.EINVAL
+    assert b"gate rows" in lib.zgdn_last_error()
     assert lib.zgdn_sigmoid_fwd(p, 5, p, 0, 10, 1.0, None) == native.EINVAL
     fused = [p, p, p, p, 1, p, p, p, p, p, p, p, 2, 1, 8, 128, 128, 4, 1e-6, 1.0, 0, None]
     assert lib.zgdn_fused_decode_step(*fused) == native.EUNSUPPORTED and b"Hv/Hk=8" in lib.zgdn_last_error()

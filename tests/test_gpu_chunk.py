@@ -93,3 +93,48 @@ def test_chunked_equals_recurrent_kernel_and_in_place(gdn, cuda):
     torch.cuda.synchronize()
     assert s_c is state
     _check(o_c.cpu(), s_c.cpu(), o_r.float().cpu(), s_r.cpu())
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_rows_read_in_place_and_beta_logits(gdn, cuda, packed):
+    """q, k, v as column slices of one wider row (the conv output) and g, beta as columns of another (the
+    input projection), beta given as logits: bit-identical to the same values handed over dense with beta =
+    sigmoid(b) from the sigmoid kernel; a row stride the kernel cannot take (not a multiple of 8) is copied
+    first, same result."""
+    announce(f"chunk rows in place, beta logits, packed={packed}")
+    gen = torch.Generator().manual_seed(2401)
+    B, T, Hk, Hv = (1, 333, 2, 4) if packed else (2, 150, 2, 4)
+    width = (2 * Hk + Hv) * 128
+    conv = (0.7 * torch.randn(B, T, width + 64, generator=gen)).to(torch.bfloat16).to(cuda)
+    proj = torch.randn(B, T, 40, generator=gen).to(torch.bfloat16).to(cuda)
+    q = conv[..., : Hk * 128].unflatten(-1, (Hk, 128))
+    k = conv[..., Hk * 128: 2 * Hk * 128].unflatten(-1, (Hk, 128))
+    v = conv[..., 2 * Hk * 128: width].unflatten(-1, (Hv, 128))
+    a, b = proj[..., 3: 3 + Hv], proj[..., 20: 20 + Hv]
+    A_log, dt_bias = (0.3 * torch.randn(Hv, generator=gen)).to(cuda), (0.3 * torch.randn(Hv, generator=gen)).to(cuda)
+    s0 = (0.02 * torch.randn(B if not packed else 3, Hv, 128, 128, generator=gen)).to(cuda)
+    kw = dict(A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=True)
+    if packed:
+        cu = torch.tensor([0, 100, 100 + 64, T], dtype=torch.int32, device=cuda)
+        kw["cu_seqlens"] = cu
+    o1, s1 = gdn.chunk_fwd(q, k, v, a, b, initial_state=s0, beta_is_logit=True, **kw)
+    beta = gdn.ops.sigmoid(b.contiguous(), out_dtype=torch.float32)
+    o2, s2 = gdn.chunk_fwd(q.contiguous(), k.contiguous(), v.contiguous(), a.float().contiguous(), beta,
+                           initial_state=s0, **kw)
+    wide = torch.zeros(B, T, width + 4, dtype=torch.bfloat16, device=cuda)  # row stride 4 mod 8: copied
+    wide[..., :width] = conv[..., :width]
+    qm = wide[..., : Hk * 128].unflatten(-1, (Hk, 128))
+    o3, s3 = gdn.chunk_fwd(qm, k, v, a, b, initial_state=s0, beta_is_logit=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    assert torch.equal(o1, o3) and torch.equal(s1, s3)
+    # and the values themselves against the oracle, sequence by sequence
+    g_log = -A_log.exp().cpu() * F.softplus(a.float().cpu() + dt_bias.cpu())
+    qn, kn = O.l2norm(q.float().cpu()), O.l2norm(k.float().cpu())
+    bounds = [(0, 100), (100, 164), (164, T)] if packed else None
+    for i in range(len(s0)):
+        bi, (lo, hi) = (0, bounds[i]) if packed else (i, (0, T))
+        o_ref, s_ref = O.gated_delta_recurrence(qn[bi:bi + 1, lo:hi], kn[bi:bi + 1, lo:hi],
+                                                v[bi:bi + 1, lo:hi].float().cpu(), g_log[bi:bi + 1, lo:hi],
+                                                beta.cpu()[bi:bi + 1, lo:hi], None, s0[i:i + 1].cpu())
+        _check(o1[bi:bi + 1, lo:hi].cpu(), s1[i:i + 1].cpu(), o_ref, s_ref)

@@ -104,3 +104,33 @@ def test_fused_l2norm_and_gate(gdn, cuda, path):
     assert rel_err(s.cpu(), s_ref) < 1e-3, rel_err(s.cpu(), s_ref)
     if path == "recurrent":
         assert rel_err(s.cpu(), s_ref) < 1e-5  # the recurrent kernel is plain fp32 arithmetic
+
+
+def test_rows_read_in_place(gdn, cuda):
+    """The conv's input, the L2 norm's rows and the gated norm's gate as column slices of wider rows (the
+    input projection, the conv output): bit-identical to the same values handed over dense. The conv input
+    also at an odd element offset (no channel pairs) and as packed sequences with states."""
+    announce("row kernels read slices in place")
+    gen = torch.Generator().manual_seed(3101)
+    T, D = 150, 96
+    buf = torch.randn(1, T, 260, generator=gen).to(torch.bfloat16).to(cuda)
+    w = (0.3 * torch.randn(D, 4, generator=gen)).to(torch.bfloat16).to(cuda)
+    s0 = torch.randn(2, D, 4, generator=gen).to(torch.bfloat16).to(cuda)
+    cu = torch.tensor([0, 70, T], dtype=torch.int32, device=cuda)
+    for off in (0, 1):
+        x = buf[..., off: off + D]
+        for kw in (dict(state_width=3), dict(initial_state=s0, cu_seqlens=cu, state_width=4)):
+            y1, f1 = gdn.ops.causal_conv1d(x, w, activation="silu", **kw)
+            y2, f2 = gdn.ops.causal_conv1d(x.contiguous(), w, activation="silu", **kw)
+            assert torch.equal(y1, y2) and torch.equal(f1, f2), (off, sorted(kw))
+    rows = buf[0, :, :256].unflatten(-1, (2, 128))  # [T, 2, 128], token stride 260
+    for dt in (torch.float32, torch.bfloat16):
+        y1, r1 = gdn.ops.l2norm(rows, out_dtype=dt)
+        y2, r2 = gdn.ops.l2norm(rows.contiguous(), out_dtype=dt)
+        assert torch.equal(y1, y2) and torch.equal(r1, r2)
+    o = torch.randn(T, 2, 128, generator=gen).to(torch.bfloat16).to(cuda)
+    nw = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16).to(cuda)
+    g1, _ = gdn.ops.gated_rmsnorm(o, rows, nw, eps=1e-5)
+    g2, _ = gdn.ops.gated_rmsnorm(o, rows.contiguous(), nw, eps=1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(g1, g2)

@@ -224,3 +224,30 @@ def test_static_decode_graph_replays_equal_eager_steps(serving, cuda):
         assert torch.equal(static_y, y_eager), step
         for name in ("_live_state", "_live_conv", "_window", "_win_len", "_recurrent_state", "_conv_state"):
             assert torch.equal(getattr(a.layer, name), getattr(b.layer, name)), (step, name)
+
+
+def test_in_place_route_equals_the_operator_seam(serving, cuda):
+    """With the package's own five operators bound, ``_run_packed`` skips the seam's copies (slices of the
+    projection and conv output read in place, sigmoid(b) in the chunked kernel): outputs and final states
+    are bit-identical to the seam route, which runs as soon as any operator attribute is rebound."""
+    announce("serving _run_packed: in-place route vs the operator seam, 3 packed requests")
+    gen = torch.Generator().manual_seed(4501)
+    d = _Driver(serving, _weights(4500, torch.bfloat16), cuda, capacity=3)
+    layer = d.layer
+    fla = importlib.import_module("zonos3-mini_amd.fla_ops")
+    lengths = [70, 1, 130]
+    x = torch.randn(sum(lengths), HIDDEN, generator=gen).to(torch.bfloat16).to(cuda)
+    cu, chunks = serving.chunk_tables(lengths, cuda)
+    conv = (0.3 * torch.randn(3, 1536, 4, generator=gen)).to(torch.bfloat16).to(cuda)
+    rec = (0.02 * torch.randn(3, 4, 128, 128, generator=gen)).to(cuda)
+    valid = (torch.rand(sum(lengths), generator=gen) > 0.2).to(cuda)
+    for keep in (None, valid):
+        assert layer._own_operators()
+        fast = layer._run_packed(x, cu, chunks, conv, rec, valid=keep, return_mixed=True)
+        layer._conv_fwd = lambda **kw: fla.causal_conv1d_fwd(**kw)  # a wrapper: the seam route runs
+        assert not layer._own_operators()
+        seam = layer._run_packed(x, cu, chunks, conv, rec, valid=keep, return_mixed=True)
+        fla.install(layer)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "conv", "state", "mixed"), fast, seam):
+            assert torch.equal(a, b), (name, keep is None)

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libzonos3_gdn.so"
 F32, BF16 = 0, 1
 # status codes (enum zgdn_status)
 OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
+ABI_VERSION = 2  # zgdn_abi_version() of the library these signatures describe
 
 _P = c_void_p
 _I32P = POINTER(c_int32)
@@ -34,7 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "zgdn_chunk_fwd": (
         c_int,
         [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int,
-         c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, c_size_t, _P],
+         c_int, c_int, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_long, c_int, c_float, _P, c_size_t,
+         _P],
     ),
     "zgdn_fused_decode_step": (
         c_int,
@@ -52,11 +54,12 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "zgdn_causal_conv1d_fwd": (
         c_int,
-        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P],
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_long,
+         _P],
     ),
-    "zgdn_l2norm_fwd": (c_int, [_P, c_int, _P, c_int, _P, c_int, c_int, c_float, _P]),
+    "zgdn_l2norm_fwd": (c_int, [_P, c_int, _P, c_int, _P, c_int, c_int, c_int, c_long, c_float, _P]),
     "zgdn_sigmoid_fwd": (c_int, [_P, c_int, _P, c_int, c_size_t, c_float, _P]),
-    "zgdn_gated_rmsnorm_fwd": (c_int, [_P, _P, _P, c_int, _P, _P, c_int, c_int, c_float, _P]),
+    "zgdn_gated_rmsnorm_fwd": (c_int, [_P, _P, _P, c_int, _P, _P, c_int, c_int, c_int, c_long, c_float, _P]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -80,7 +83,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.zgdn_abi_version() != 1:
+        if handle.zgdn_abi_version() != ABI_VERSION:
             raise RuntimeError("libzonos3_gdn.so ABI version mismatch; rebuild it")
         _lib = handle
     return _lib

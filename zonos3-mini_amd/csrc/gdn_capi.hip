@@ -33,4 +33,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* zgdn_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int zgdn_abi_version(void) { return 1; }
+extern "C" int zgdn_abi_version(void) { return 2; }

@@ -260,6 +260,14 @@ __device__ __forceinline__ void zero_upper_blocks(uint16_t* m) {
 // Contraction length over tokens for token tile tb of a lower-triangular left operand.
 __device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
 
+// Elements between consecutive tokens of q, k, v and of g / beta (a token's heads are contiguous in each), so
+// that the kernel reads column slices of wider rows (the conv output, the input projection) in place;
+// beta_sigmoid: beta holds the raw input b and the kernel takes sigmoid(b) (in fp32).
+struct RowStrides {
+  long q, k, v, gb;
+  int beta_sigmoid;
+};
+
 // Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
 // Two workgroups share a CU, so one's loads and barriers overlap the other's work.
 template <typename TG, bool GATE>
@@ -267,7 +275,8 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
-    int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, uint8_t* __restrict__ ws) {
+    int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
+    uint8_t* __restrict__ ws) {
   __shared__ Prep sm;
   const int wave = threadIdx.x >> 6;
 
@@ -290,15 +299,15 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
       uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
       if (r0 < cr.len) {
         const size_t t = (size_t)(cr.t0 + r0);
-        q0 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
-        k0 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
-        v0 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
+        q0 = *reinterpret_cast<const uint4*>(q + t * rs.q + hk * DK + c8);
+        k0 = *reinterpret_cast<const uint4*>(k + t * rs.k + hk * DK + c8);
+        v0 = *reinterpret_cast<const uint4*>(v + t * rs.v + h * DV + c8);
       }
       if (r1 < cr.len) {
         const size_t t = (size_t)(cr.t0 + r1);
-        q1 = *reinterpret_cast<const uint4*>(q + (t * Hk + hk) * DK + c8);
-        k1 = *reinterpret_cast<const uint4*>(k + (t * Hk + hk) * DK + c8);
-        v1 = *reinterpret_cast<const uint4*>(v + (t * Hv + h) * DV + c8);
+        q1 = *reinterpret_cast<const uint4*>(q + t * rs.q + hk * DK + c8);
+        k1 = *reinterpret_cast<const uint4*>(k + t * rs.k + hk * DK + c8);
+        v1 = *reinterpret_cast<const uint4*>(v + t * rs.v + h * DV + c8);
       }
       *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r0, c8)]) = q0;
       *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r1, c8)]) = q1;
@@ -310,10 +319,11 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     if (wave == P1_WAVES - 1) {
       float gi = 0.f, bi = 0.f;
       if (l < cr.len) {
-        const size_t gh = (size_t)(cr.t0 + l) * Hv + h;
+        const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
         gi = io<TG>::load(g + gh);
         if constexpr (GATE) gi = -__expf(A_log[h]) * softplus(gi + dt_bias[h]);
         bi = io<TG>::load(beta + gh);
+        if (rs.beta_sigmoid) bi = sigmoid(bi);
       }
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
@@ -485,7 +495,7 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
       const int tok = 16 * tb + (l & 15);
       cq[m][0] = cq[m][1] = make_uint2(0, 0);
       if (tok < cr.len) {
-        const uint16_t* qrow = q + ((size_t)(cr.t0 + tok) * Hk + hk) * DK + 32 * kq + 4 * (l >> 4);
+        const uint16_t* qrow = q + (size_t)(cr.t0 + tok) * rs.q + hk * DK + 32 * kq + 4 * (l >> 4);
         cq[m][0] = *reinterpret_cast<const uint2*>(qrow);
         cq[m][1] = *reinterpret_cast<const uint2*>(qrow + 16);
       }
@@ -770,8 +780,8 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 template <typename TG>
 void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const void* k, const void* v, const void* g,
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
-                 const int32_t* chunk_idx, int n_seqs, int T, float scale, int qk_l2norm, uint8_t* ws,
-                 hipStream_t stream) {
+                 const int32_t* chunk_idx, int n_seqs, int T, float scale, int qk_l2norm, const RowStrides& rs,
+                 uint8_t* ws, hipStream_t stream) {
   // P1_WGS_PER_CU resident workgroups per CU (what the LDS footprint allows), each looping over items
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -781,11 +791,11 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
   if (gate)
     hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, ws);
+                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, rs, ws);
   else
     hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, ws);
+                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, rs, ws);
 }
 
 }  // namespace
@@ -799,8 +809,9 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
                               const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
                               int qk_l2norm, const float* initial_state, float* final_state, void* o,
                               const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
-                              int B, int T, int Hk, int Hv, int K, int V, float scale, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+                              int B, int T, int Hk, int Hv, int K, int V, long q_ld, long k_ld, long v_ld,
+                              long gb_ld, int beta_sigmoid, float scale, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_chunk_fwd";
   if (!q || !k || !v || !g || !beta || !o || !workspace) return fail(ZGDN_EINVAL, "%s: null pointer", fn);
@@ -811,6 +822,13 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
     return fail(ZGDN_EINVAL, "%s: bad sizes B=%d T=%d Hk=%d Hv=%d", fn, B, T, Hk, Hv);
   if ((A_log == nullptr) != (dt_bias == nullptr))
     return fail(ZGDN_EINVAL, "%s: A_log and dt_bias go together", fn);
+  // row strides: at least a token's heads; q / k / v rows start on 16-byte boundaries (the kernel reads
+  // 8-element groups)
+  if (q_ld < (long)Hk * K || k_ld < (long)Hk * K || v_ld < (long)Hv * V || gb_ld < Hv || q_ld % 8 || k_ld % 8 ||
+      v_ld % 8 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16)
+    return fail(ZGDN_EINVAL, "%s: row strides q=%ld k=%ld v=%ld g/beta=%ld (need >= a token's heads, q/k/v "
+                "multiples of 8 elements from 16-byte aligned bases)", fn, q_ld, k_ld, v_ld, gb_ld);
+  const RowStrides rs{q_ld, k_ld, v_ld, gb_ld, beta_sigmoid != 0};
   int N = B;
   if (cu_seqlens != nullptr) {
     if (B != 1 || chunk_indices == nullptr || n_seqs < 1)
@@ -829,10 +847,10 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
   if (n_chunks > 0) {
     if (gb_dtype == ZGDN_F32)
       launch_prep<float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                               N, T, scale, qk_l2norm, ws, s);
+                               N, T, scale, qk_l2norm, rs, ws, s);
     else
       launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                              N, T, scale, qk_l2norm, ws, s);
+                              N, T, scale, qk_l2norm, rs, ws, s);
   }
   dim3 grid2(((N * Hv + 7) / 8) * 64);  // groups of 8 (sequence, head) pairs x DV / VB = 8 value blocks
   hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,

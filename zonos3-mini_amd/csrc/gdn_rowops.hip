@@ -62,7 +62,7 @@ struct chans<float, 2> {
 };
 
 // y[t, c] = act(sum_j w[c, j] * x_{t - W + 1 + j}[c] + bias[c]) over CONV_TT tokens of one chunk of one
-// sequence, CPT channels per thread, with x_{<0} taken from the sequence's history (the last W-1 columns of
+// sequence (x rows x_ld elements apart, y rows dense), CPT channels per thread, with x_{<0} taken from the sequence's history (the last W-1 columns of
 // its state row, oldest first); the first tile of a sequence also writes the new state row = the last SW raw
 // inputs of [history | x]. The accumulation is fp32; like F.conv1d and F.silu on `T` tensors, the conv
 // result is rounded to T before the activation and the activation after. A tile issues all its token loads
@@ -71,7 +71,7 @@ template <typename T, int CPT, int WK>
 __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, const T* init, T* fin,
     T* __restrict__ y, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx, int n_seqs,
-    int n_chunks, int T_len, int D, int W_arg, int SW, int act) {
+    int n_chunks, int T_len, int D, long x_ld, int W_arg, int SW, int act) {
   const int W = WK > 0 ? WK : W_arg;  // WK: the width as a constant (the model's 4), 0: taken at run time
   const int c0 = (blockIdx.y * CONV_THREADS + threadIdx.x) * CPT;
   if (c0 >= D) return;
@@ -134,12 +134,12 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
     br[k] = (bias != nullptr ? bias : w)[bias != nullptr ? c : 0];
   }
 #pragma unroll
-  for (int i = 0; i < CONV_TT; ++i) xr[i] = C::load(x + ((size_t)(bos + min(t0 + i, last))) * D + c0);
+  for (int i = 0; i < CONV_TT; ++i) xr[i] = C::load(x + ((size_t)(bos + min(t0 + i, last))) * x_ld + c0);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const T* xc = x + (size_t)bos * D + c0 + k;
+    const T* xc = x + (size_t)bos * x_ld + c0 + k;
 #pragma unroll
-    for (int i = 0; i < CONV_WMAX; ++i) hx[k][i] = xc[(size_t)min(max(t0 - (W - 1) + i, 0), last) * D];
+    for (int i = 0; i < CONV_WMAX; ++i) hx[k][i] = xc[(size_t)min(max(t0 - (W - 1) + i, 0), last) * x_ld];
   }
   if (init != nullptr && (t0 < W - 1 || writes_state)) {
 #pragma unroll
@@ -155,9 +155,9 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
   if (writes_state) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const T* xc = x + (size_t)bos * D + c0 + k;
+      const T* xc = x + (size_t)bos * x_ld + c0 + k;
 #pragma unroll
-      for (int i = 0; i < CONV_WMAX; ++i) nx[k][i] = xc[(size_t)min(max(len - SW + i, 0), last) * D];
+      for (int i = 0; i < CONV_WMAX; ++i) nx[k][i] = xc[(size_t)min(max(len - SW + i, 0), last) * x_ld];
     }
   }
   // values used (a missing state row reads as zeros)
@@ -214,14 +214,130 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
   }
 }
 
-// y = x * rsqrt(sum x^2 + eps) over rows of D <= 1024 elements; one wave per row.
+// Rows of 128 (the head size): 16 lanes per row, each with 8 consecutive elements in one 16-byte access
+// (two for fp32; element by element where some row is not 16-byte aligned, ALIGNED false, with the same
+// arithmetic, so results do not depend on where the rows sit; every D = 128 call runs these kernels), and the row sum over the 16 lanes by DPP;
+// four rows per wave.
+template <typename T>
+struct oct;
+template <>
+struct oct<bf16> {
+  using raw = uint4;
+  __device__ __forceinline__ static raw load(const bf16* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ static raw load_unaligned(const bf16* p) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = (uint32_t)p[2 * i].bits | ((uint32_t)p[2 * i + 1].bits << 16);
+    return make_uint4(u[0], u[1], u[2], u[3]);
+  }
+  __device__ __forceinline__ static void unpack(const raw& w, float* v) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(u[i] << 16);
+      v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static void store(bf16* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                              pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  }
+  __device__ __forceinline__ static void store_unaligned(bf16* p, const float* v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) io<bf16>::store(p + i, v[i]);
+  }
+};
+template <>
+struct oct<float> {
+  struct raw {
+    float4 a, b;
+  };
+  __device__ __forceinline__ static raw load(const float* p) {
+    return {reinterpret_cast<const float4*>(p)[0], reinterpret_cast<const float4*>(p)[1]};
+  }
+  __device__ __forceinline__ static raw load_unaligned(const float* p) {
+    return {make_float4(p[0], p[1], p[2], p[3]), make_float4(p[4], p[5], p[6], p[7])};
+  }
+  __device__ __forceinline__ static void unpack(const raw& w, float* v) {
+    v[0] = w.a.x, v[1] = w.a.y, v[2] = w.a.z, v[3] = w.a.w;
+    v[4] = w.b.x, v[5] = w.b.y, v[6] = w.b.z, v[7] = w.b.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  __device__ __forceinline__ static void store_unaligned(float* p, const float* v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = v[i];
+  }
+};
+constexpr int R128_ROWS = 16;  // rows per 256-thread workgroup
+
+// A whole 16-lane group exits together, so the DPP sums read active lanes only.
+template <typename TI, typename TO, bool ALIGNED>
+__global__ __launch_bounds__(256) void l2norm128_kernel(const TI* __restrict__ x, TO* __restrict__ y,
+                                                        float* __restrict__ rstd, int rows, int x_group,
+                                                        long x_ld, float eps) {
+  const int row = blockIdx.x * R128_ROWS + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+  if (row >= rows) return;
+  const TI* xr = x + (size_t)(row / x_group) * x_ld + (size_t)(row % x_group) * 128 + 8 * sub;
+  float v[8];
+  oct<TI>::unpack(ALIGNED ? oct<TI>::load(xr) : oct<TI>::load_unaligned(xr), v);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  const float r = rsqrtf(group_sum<16>(ss) + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] *= r;
+  TO* yr = y + (size_t)row * 128 + 8 * sub;
+  if constexpr (ALIGNED) oct<TO>::store(yr, v);
+  else oct<TO>::store_unaligned(yr, v);
+  if (rstd != nullptr && sub == 0) rstd[row] = r;
+}
+
+template <typename T, bool ALIGNED>
+__global__ __launch_bounds__(256) void gated_rmsnorm128_kernel(const T* __restrict__ x, const T* __restrict__ g,
+                                                               const T* __restrict__ w, T* __restrict__ y,
+                                                               float* __restrict__ rstd, int rows, int g_group,
+                                                               long g_ld, float eps) {
+  const int row = blockIdx.x * R128_ROWS + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+  if (row >= rows) return;
+  const T* xp = x + (size_t)row * 128 + 8 * sub;
+  const T* gp = g + (size_t)(row / g_group) * g_ld + (size_t)(row % g_group) * 128 + 8 * sub;
+  const typename oct<T>::raw xr = ALIGNED ? oct<T>::load(xp) : oct<T>::load_unaligned(xp);
+  const typename oct<T>::raw gr = ALIGNED ? oct<T>::load(gp) : oct<T>::load_unaligned(gp);
+  const typename oct<T>::raw wr = ALIGNED ? oct<T>::load(w + 8 * sub) : oct<T>::load_unaligned(w + 8 * sub);
+  float v[8], gv[8], wv[8];
+  oct<T>::unpack(xr, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  const float r = rsqrtf(group_sum<16>(ss) / 128.f + eps);
+  oct<T>::unpack(gr, gv);
+  oct<T>::unpack(wr, wv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = rnd<T>(v[i] * r * wv[i]) * silu(gv[i]);
+  T* yr = y + (size_t)row * 128 + 8 * sub;
+  if constexpr (ALIGNED) oct<T>::store(yr, v);
+  else oct<T>::store_unaligned(yr, v);
+  if (rstd != nullptr && sub == 0) rstd[row] = r;
+}
+
+// Whether rows of 128 at base p, ld elements apart, suit the 16-byte accesses of the 128-wide kernels.
+__host__ inline bool rows128(const void* p, long ld, size_t esz) {
+  return (uintptr_t)p % 16 == 0 && (ld * (long)esz) % 16 == 0;
+}
+
+// y = x * rsqrt(sum x^2 + eps) over rows of D <= 1024 elements; one wave per row. y is dense; row r of x
+// starts at x + (r / x_group) * x_ld + (r % x_group) * D (a token's per-head rows inside a wider row).
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void l2norm_kernel(const TI* __restrict__ x, TO* __restrict__ y,
-                                                     float* __restrict__ rstd, int rows, int D, float eps) {
+                                                     float* __restrict__ rstd, int rows, int D, int x_group,
+                                                     long x_ld, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const TI* xr = x + (size_t)row * D;
+  const TI* xr = x + (size_t)(row / x_group) * x_ld + (size_t)(row % x_group) * D;
   float v[16];
   float ss = 0.f;
 #pragma unroll
@@ -247,11 +363,14 @@ __global__ __launch_bounds__(256) void sigmoid_kernel(const TI* __restrict__ x, 
   if (i < n) io<TO>::store(y + i, sigmoid(io<TI>::load(x + i)) * scale);
 }
 
-// y = (rms_norm(x) * w).to(T) * silu(g), product in fp32, cast to T; one wave per row of D <= 1024.
+// y = (rms_norm(x) * w).to(T) * silu(g), product in fp32, cast to T; one wave per row of D <= 1024. x and y
+// are dense; row r's gate starts at g + (r / g_group) * g_ld + (r % g_group) * D (per-head rows of a token's
+// gate, read in place from a wider row).
 template <typename T>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ x, const T* __restrict__ g,
                                                             const T* __restrict__ w, T* __restrict__ y,
-                                                            float* __restrict__ rstd, int rows, int D, float eps) {
+                                                            float* __restrict__ rstd, int rows, int D, int g_group,
+                                                            long g_ld, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -265,7 +384,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
     ss = fmaf(v[i], v[i], ss);
   }
   const float r = rsqrtf(wave_sum(ss) / (float)D + eps);
-  const T* gr = g + (size_t)row * D;
+  const T* gr = g + (size_t)(row / g_group) * g_ld + (size_t)(row % g_group) * D;
   T* yr = y + (size_t)row * D;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -281,10 +400,12 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
 extern "C" int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, int dtype,
                                       const void* initial_state, void* final_state, int state_width, void* y,
                                       const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs,
-                                      int n_chunks, int B, int T, int D, int W, int activation, void* stream) {
+                                      int n_chunks, int B, int T, int D, int W, int activation, long x_ld,
+                                      void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_causal_conv1d_fwd";
   if (!x || !weight || !y) return fail(ZGDN_EINVAL, "%s: null pointer", fn);
+  if (x_ld < D) return fail(ZGDN_EINVAL, "%s: x row stride %ld < D=%d", fn, x_ld, D);
   if (W < 1 || W > CONV_WMAX) return fail(ZGDN_EUNSUPPORTED, "%s: width %d (supported: 1..4)", fn, W);
   if (state_width < W - 1 || state_width > CONV_WMAX)
     return fail(ZGDN_EINVAL, "%s: state width %d for conv width %d (need W-1 .. 4)", fn, state_width, W);
@@ -310,11 +431,13 @@ extern "C" int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const v
     auto kernel = W == 4 ? conv_kernel<TT, CPT, 4> : conv_kernel<TT, CPT, 0>;
     hipLaunchKernelGGL(kernel, grid, dim3(CONV_THREADS), 0, s, (const TT*)x, (const TT*)weight, (const TT*)bias,
                        (const TT*)initial_state, (TT*)final_state, (TT*)y, cu_seqlens, chunk_indices, n_seqs,
-                       n_chunks, T, D, W, state_width, activation);
+                       n_chunks, T, D, x_ld, W, state_width, activation);
   };
   using One = std::integral_constant<int, 1>;
   using Two = std::integral_constant<int, 2>;
-  const bool pairs = D % 2 == 0;  // two channels per thread keep each pair 4- or 8-byte aligned
+  // two channels per thread where every pair of x and y stays 4- or 8-byte aligned
+  const size_t esz = dtype == ZGDN_F32 ? 4 : 2;
+  const bool pairs = D % 2 == 0 && x_ld % 2 == 0 && (uintptr_t)x % (2 * esz) == 0 && (uintptr_t)y % (2 * esz) == 0;
   if (dtype == ZGDN_F32) {
     if (pairs) go((float*)nullptr, Two{});
     else go((float*)nullptr, One{});
@@ -326,24 +449,42 @@ extern "C" int zgdn_causal_conv1d_fwd(const void* x, const void* weight, const v
 }
 
 extern "C" int zgdn_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd, int rows, int D,
-                               float eps, void* stream) {
+                               int x_group, long x_ld, float eps, void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_l2norm_fwd";
   if (!x || !y) return fail(ZGDN_EINVAL, "%s: null pointer", fn);
   if (rows < 0 || D < 1 || D > 1024) return fail(ZGDN_EUNSUPPORTED, "%s: rows=%d D=%d (D <= 1024)", fn, rows, D);
+  if (x_group < 1 || x_ld < (long)x_group * D)
+    return fail(ZGDN_EINVAL, "%s: x rows: group %d, stride %ld (need group >= 1, stride >= group * D)", fn,
+                x_group, x_ld);
   for (int dt : {x_dtype, y_dtype})
     if (dt != ZGDN_F32 && dt != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, dt);
   if (rows == 0) return check_launch(fn);
-  dim3 grid((rows + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
+  if (D == 128) {
+    const bool al = rows128(x, x_ld, x_dtype == ZGDN_F32 ? 4 : 2) && rows128(y, 128, y_dtype == ZGDN_F32 ? 4 : 2);
+    dim3 grid((rows + R128_ROWS - 1) / R128_ROWS), block(256);
+    auto go = [&](auto* ti, auto* to) {
+      using TI = std::remove_const_t<std::remove_pointer_t<decltype(ti)>>;
+      using TO = std::remove_pointer_t<decltype(to)>;
+      auto kernel = al ? l2norm128_kernel<TI, TO, true> : l2norm128_kernel<TI, TO, false>;
+      hipLaunchKernelGGL(kernel, grid, block, 0, s, (const TI*)x, (TO*)y, rstd, rows, x_group, x_ld, eps);
+    };
+    if (x_dtype == ZGDN_F32 && y_dtype == ZGDN_F32) go((float*)nullptr, (float*)nullptr);
+    else if (x_dtype == ZGDN_F32) go((float*)nullptr, (bf16*)nullptr);
+    else if (y_dtype == ZGDN_F32) go((bf16*)nullptr, (float*)nullptr);
+    else go((bf16*)nullptr, (bf16*)nullptr);
+    return check_launch(fn);
+  }
+  dim3 grid((rows + 3) / 4), block(256);
   if (x_dtype == ZGDN_F32 && y_dtype == ZGDN_F32)
-    hipLaunchKernelGGL((l2norm_kernel<float, float>), grid, block, 0, s, (const float*)x, (float*)y, rstd, rows, D, eps);
+    hipLaunchKernelGGL((l2norm_kernel<float, float>), grid, block, 0, s, (const float*)x, (float*)y, rstd, rows, D, x_group, x_ld, eps);
   else if (x_dtype == ZGDN_F32)
-    hipLaunchKernelGGL((l2norm_kernel<float, bf16>), grid, block, 0, s, (const float*)x, (bf16*)y, rstd, rows, D, eps);
+    hipLaunchKernelGGL((l2norm_kernel<float, bf16>), grid, block, 0, s, (const float*)x, (bf16*)y, rstd, rows, D, x_group, x_ld, eps);
   else if (y_dtype == ZGDN_F32)
-    hipLaunchKernelGGL((l2norm_kernel<bf16, float>), grid, block, 0, s, (const bf16*)x, (float*)y, rstd, rows, D, eps);
+    hipLaunchKernelGGL((l2norm_kernel<bf16, float>), grid, block, 0, s, (const bf16*)x, (float*)y, rstd, rows, D, x_group, x_ld, eps);
   else
-    hipLaunchKernelGGL((l2norm_kernel<bf16, bf16>), grid, block, 0, s, (const bf16*)x, (bf16*)y, rstd, rows, D, eps);
+    hipLaunchKernelGGL((l2norm_kernel<bf16, bf16>), grid, block, 0, s, (const bf16*)x, (bf16*)y, rstd, rows, D, x_group, x_ld, eps);
   return check_launch(fn);
 }
 
@@ -369,20 +510,38 @@ extern "C" int zgdn_sigmoid_fwd(const void* x, int x_dtype, void* y, int y_dtype
 }
 
 extern "C" int zgdn_gated_rmsnorm_fwd(const void* x, const void* g, const void* weight, int dtype, void* y,
-                                      float* rstd, int rows, int D, float eps, void* stream) {
+                                      float* rstd, int rows, int D, int g_group, long g_ld, float eps,
+                                      void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_gated_rmsnorm_fwd";
   if (!x || !g || !weight || !y) return fail(ZGDN_EINVAL, "%s: null pointer", fn);
+  if (g_group < 1 || g_ld < (long)g_group * D)
+    return fail(ZGDN_EINVAL, "%s: gate rows: group %d, stride %ld (need group >= 1, stride >= group * D)", fn,
+                g_group, g_ld);
   if (rows < 0 || D < 1 || D > 1024) return fail(ZGDN_EUNSUPPORTED, "%s: rows=%d D=%d (D <= 1024)", fn, rows, D);
   if (dtype != ZGDN_F32 && dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, dtype);
   if (rows == 0) return check_launch(fn);
-  dim3 grid((rows + 3) / 4), block(256);
   hipStream_t s = (hipStream_t)stream;
+  const size_t esz = dtype == ZGDN_F32 ? 4 : 2;
+  if (D == 128) {
+    const bool al = rows128(x, 128, esz) && rows128(g, g_ld, esz) && rows128(weight, 0, esz) && rows128(y, 128, esz);
+    dim3 grid((rows + R128_ROWS - 1) / R128_ROWS), block(256);
+    auto go = [&](auto* tag) {
+      using T = std::remove_pointer_t<decltype(tag)>;
+      auto kernel = al ? gated_rmsnorm128_kernel<T, true> : gated_rmsnorm128_kernel<T, false>;
+      hipLaunchKernelGGL(kernel, grid, block, 0, s, (const T*)x, (const T*)g, (const T*)weight, (T*)y, rstd, rows,
+                         g_group, g_ld, eps);
+    };
+    if (dtype == ZGDN_F32) go((float*)nullptr);
+    else go((bf16*)nullptr);
+    return check_launch(fn);
+  }
+  dim3 grid((rows + 3) / 4), block(256);
   if (dtype == ZGDN_F32)
     hipLaunchKernelGGL(gated_rmsnorm_kernel<float>, grid, block, 0, s, (const float*)x, (const float*)g,
-                       (const float*)weight, (float*)y, rstd, rows, D, eps);
+                       (const float*)weight, (float*)y, rstd, rows, D, g_group, g_ld, eps);
   else
     hipLaunchKernelGGL(gated_rmsnorm_kernel<bf16>, grid, block, 0, s, (const bf16*)x, (const bf16*)g,
-                       (const bf16*)weight, (bf16*)y, rstd, rows, D, eps);
+                       (const bf16*)weight, (bf16*)y, rstd, rows, D, g_group, g_ld, eps);
   return check_launch(fn);
 }

@@ -42,12 +42,8 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
     dev, dt = x.device, x.dtype
     projection = self._lin(p + "in_proj", x, a.in_proj.weight)
     qkv, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
-    history = cache.conv_state.get(layer)
-    if history is None:
-        history = torch.zeros(channels, kernel - 1, dtype=dt, device=dev)
+    history = cache.conv_state.get(layer)  # None before the first call: the kernels read zeros
     state = cache.gdn_state.get(layer)
-    if state is None:
-        state = torch.zeros(heads, hd, hd, dtype=torch.float32, device=dev)
     A_log, dt_bias = a.A_log.float().contiguous(), a.dt_bias.float().contiguous()
     conv_w = conv_w.to(dt).contiguous()
     norm_w = a.out_weight.to(dt).contiguous()
@@ -55,8 +51,14 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
 
     if n == 1 and hd == 128 and kernel == 4 and not capture:
         # the fused decode block updates conv history and state in place: work on fresh copies
-        new_hist = history.reshape(1, channels, kernel - 1).clone()
-        new_state = state.reshape(1, heads, hd, hd).float().clone()
+        if history is None:
+            new_hist = torch.zeros(1, channels, kernel - 1, dtype=dt, device=dev)
+        else:
+            new_hist = history.reshape(1, channels, kernel - 1).clone()
+        if state is None:
+            new_state = torch.zeros(1, heads, hd, hd, dtype=torch.float32, device=dev)
+        else:
+            new_state = state.reshape(1, heads, hd, hd).float().clone()
         gated = ops.fused_decode_step(qkv.contiguous(), z.reshape(1, heads, hd).contiguous(),
                                       aa.contiguous(), b.contiguous(), conv_w, new_hist, new_state, norm_w, A_log,
                                       dt_bias, eps=1e-5)
@@ -64,30 +66,34 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
         cache.gdn_state[layer] = new_state.reshape(heads, hd, hd)
         return self._lin(p + "wo", gated.reshape(1, inner), a.wo.weight)
 
-    conv, new_hist = ops.causal_conv1d(qkv.contiguous().unsqueeze(0), conv_w,
-                                       initial_state=history.reshape(1, channels, kernel - 1).contiguous(),
-                                       activation="silu", state_width=kernel - 1)
-    conv = conv[0]
-    q, k, v = (part.reshape(1, n, heads, hd).contiguous() for part in conv.split(inner, -1))
-    g_raw = aa.float().reshape(1, n, heads).contiguous()
-    beta = ops.sigmoid(b.contiguous(), out_dtype=torch.float32).reshape(1, n, heads)
-    s0 = state.reshape(1, heads, hd, hd).float().contiguous()
+    # q|k|v, z, a and b are read in place from the projection rows; the conv output's q, k, v column slices
+    # likewise
+    h0 = None if history is None else history.reshape(1, channels, kernel - 1).contiguous()
+    conv, new_hist = ops.causal_conv1d(qkv.unsqueeze(0), conv_w, initial_state=h0, activation="silu",
+                                       state_width=kernel - 1)
+    q, k, v = (part.unflatten(-1, (heads, hd)) for part in conv.split(inner, -1))
+    s0 = None if state is None else state.reshape(1, heads, hd, hd).float().contiguous()
     kw = dict(initial_state=s0, A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=True)
     if dt == torch.bfloat16 and hd == 128:
-        o, new_state = ops.chunk_fwd(q, k, v, g_raw, beta, **kw)
+        o, new_state = ops.chunk_fwd(q, k, v, aa.unsqueeze(0), b.unsqueeze(0), beta_is_logit=True, **kw)
+        beta = None
     else:
-        o, new_state = ops.recurrent_fwd(q, k, v, g_raw, beta, out_dtype=dt, **kw)
+        beta = ops.sigmoid(b.contiguous(), out_dtype=torch.float32).reshape(1, n, heads)
+        o, new_state = ops.recurrent_fwd(q.contiguous(), k.contiguous(), v.contiguous(),
+                                         aa.float().reshape(1, n, heads).contiguous(), beta, out_dtype=dt, **kw)
     recurrent = o.reshape(n, heads, hd).to(dt)
-    gated, _ = ops.gated_rmsnorm(recurrent, z.reshape(n, heads, hd).contiguous(), norm_w, eps=1e-5)
+    gated, _ = ops.gated_rmsnorm(recurrent, z.unflatten(-1, (heads, hd)), norm_w, eps=1e-5)
     gated = gated.reshape(n, inner)
     cache.conv_state[layer] = new_hist.reshape(channels, kernel - 1)
     cache.gdn_state[layer] = new_state.reshape(heads, hd, hd)
     if capture:
-        qn, _ = ops.l2norm(q.reshape(n, heads, hd), out_dtype=torch.float32)
-        kn, _ = ops.l2norm(k.reshape(n, heads, hd), out_dtype=torch.float32)
+        qn, _ = ops.l2norm(q.reshape(n, heads, hd).contiguous(), out_dtype=torch.float32)
+        kn, _ = ops.l2norm(k.reshape(n, heads, hd).contiguous(), out_dtype=torch.float32)
+        if beta is None:
+            beta = ops.sigmoid(b.contiguous(), out_dtype=torch.float32)
         decay = torch.exp(-A_log.exp() * F.softplus(aa.float() + dt_bias))  # diagnostics only
         for name, tensor in (
-            ("gdn_conv", conv), ("gdn_q", qn), ("gdn_k", kn), ("gdn_v", v.reshape(n, heads, hd).float()),
+            ("gdn_conv", conv[0]), ("gdn_q", qn), ("gdn_k", kn), ("gdn_v", v.reshape(n, heads, hd).float()),
             ("gdn_decay", decay), ("gdn_beta", beta.reshape(n, heads)), ("gdn_recurrent", recurrent),
             ("gdn_gated", gated), ("gdn_state", cache.gdn_state[layer]),
             ("gdn_conv_state", cache.conv_state[layer]),

@@ -36,6 +36,57 @@ def _on_gpu(name: str, t: torch.Tensor, device: torch.device | None = None) -> N
         _require(t.device == device, f"{name}: on {t.device}, expected {device}")
 
 
+def _row_stride(t: torch.Tensor, inner_dims: int) -> int | None:
+    """Elements between consecutive rows of ``t`` when its last ``inner_dims`` dims are one dense row and its
+    leading dims step in whole rows (a column slice of a wider row-major buffer qualifies); None otherwise."""
+    shape, stride = t.shape, t.stride()
+    lead = t.dim() - inner_dims
+    width = 1
+    for d in range(t.dim() - 1, lead - 1, -1):
+        if shape[d] != 1 and stride[d] != width:
+            return None
+        width *= shape[d]
+    ld, rows = None, 1
+    for d in range(lead - 1, -1, -1):
+        if shape[d] == 1:
+            continue
+        if ld is None:
+            ld = stride[d]
+        elif stride[d] != rows * ld:
+            return None
+        rows *= shape[d]
+    if ld is None:
+        return width
+    return ld if ld >= width else None
+
+
+def _rows_in_place(name: str, t: torch.Tensor, inner_dims: int, device, multiple: int = 1, align: int = 1):
+    """(t, row stride) when the kernels can read t's rows in place -- row stride a multiple of ``multiple``
+    elements, base aligned to ``align`` bytes -- else (a contiguous copy, dense row width)."""
+    _require(isinstance(t, torch.Tensor), f"{name}: expected a tensor")
+    _require(t.is_cuda, f"{name}: must be a GPU tensor (got device {t.device}); there is no CPU path")
+    if device is not None:
+        _require(t.device == device, f"{name}: on {t.device}, expected {device}")
+    ld = _row_stride(t, inner_dims)
+    if ld is None or ld % multiple or t.data_ptr() % align:
+        t = t.contiguous()
+        ld = _row_stride(t, inner_dims)
+    return t, ld
+
+
+def _head_rows(name: str, t: torch.Tensor, device=None):
+    """(t, group, stride) for the row kernels: t's rows of its last dim D, row r starting at
+    (r / group) * stride + (r % group) * D -- the dims after the first dense (a token's heads), the first
+    stepping by ``stride`` (a column slice of wider rows qualifies). Layouts outside that are copied first."""
+    t, ld = _rows_in_place(name, t, max(t.dim() - 1, 1) if isinstance(t, torch.Tensor) else 1, device)
+    if t.dim() < 2:
+        return t, 1, t.shape[-1] if t.dim() else 1
+    group = 1
+    for n in t.shape[1:-1]:
+        group *= n
+    return t, group, ld
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -135,25 +186,34 @@ def chunk_indices_from_cu(cu_seqlens: torch.Tensor) -> torch.Tensor:
 
 
 def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
-              chunk_indices=None, A_log=None, dt_bias=None, final_state=None, use_qk_l2norm=False):
+              chunk_indices=None, A_log=None, dt_bias=None, final_state=None, use_qk_l2norm=False,
+              beta_is_logit=False):
     """Chunked gated delta rule (64-token chunks, bf16 MFMA, fp32 state): the prefill core.
 
     The operator behind FLA's ``chunk_gated_delta_rule_fwd`` as the serving layer calls it
     (``servers/sgl/src/zonos3_sgl/models/gdn.py:418-434``): q, k [B, T, Hk, 128], v [B, T, Hv, 128] bf16;
     g, beta [B, T, Hv] float32 or bfloat16. With ``A_log``/``dt_bias`` (float32 [Hv]) g is the raw gate input
     and the decay is formed in the kernel (``use_gate_in_kernel=True``). ``use_qk_l2norm``: q, k are the raw
-    rows, L2-normalised in the kernel with fp32 factors (never rounded after the norm). Packed sequences: B == 1,
-    ``cu_seqlens`` int32 [N+1] and optionally ``chunk_indices`` int32 [n_chunks, 2]. Returns
-    (o [B, T, Hv, 128] bf16, final state [N, Hv, 128, 128] float32 or None)."""
-    _on_gpu("q", q)
-    dev = q.device
-    for name, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
-        _on_gpu(name, t, dev)
+    rows, L2-normalised in the kernel with fp32 factors (never rounded after the norm). ``beta_is_logit``: beta
+    holds the raw input b and the kernel takes sigmoid(b) in fp32 (what ``sigmoid`` returns, FLA's
+    fused_beta_sigmoid_fwd at gdn.py:423). Packed sequences: B == 1, ``cu_seqlens`` int32 [N+1] and optionally
+    ``chunk_indices`` int32 [n_chunks, 2]. q, k, v, g, beta may be column slices of wider rows (the conv output,
+    the input projection): rows whose stride the kernel can take are read in place, others are copied first.
+    Returns (o [B, T, Hv, 128] bf16, final state [N, Hv, 128, 128] float32 or None)."""
+    dev = q.device if isinstance(q, torch.Tensor) else None
+    q, q_ld = _rows_in_place("q", q, 2, dev, 8, 16)
+    k, k_ld = _rows_in_place("k", k, 2, dev, 8, 16)
+    v, v_ld = _rows_in_place("v", v, 2, dev, 8, 16)
     _require(q.dim() == 4 and k.shape == q.shape, f"q, k: expected equal [B, T, Hk, K], got {tuple(q.shape)}, "
                                                   f"{tuple(k.shape)}")
     B, T, Hk, K = q.shape
     _require(v.dim() == 4 and v.shape[:2] == (B, T), f"v: expected [B={B}, T={T}, Hv, V], got {tuple(v.shape)}")
     Hv, V = v.shape[2], v.shape[3]
+    g, gb_ld = _rows_in_place("g", g, 1, dev)
+    beta, beta_ld = _rows_in_place("beta", beta, 1, dev)
+    if beta_ld != gb_ld:  # one row stride serves both
+        g, gb_ld = g.contiguous(), Hv
+        beta = beta.contiguous()
     _require(K == 128 and V == 128, f"chunk_fwd: head dims K={K}, V={V}; the chunked kernel needs 128")
     _require(Hv % Hk == 0, f"value heads ({Hv}) must be a multiple of key heads ({Hk})")
     _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "chunk_fwd: q, k, v must be bfloat16")
@@ -192,8 +252,8 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
         "zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), BF16, g.data_ptr(), beta.data_ptr(), gb_code,
         _ptr(A_log), _ptr(dt_bias), int(bool(use_qk_l2norm)), _ptr(initial_state), _ptr(final_state), o.data_ptr(),
         _ptr(cu_seqlens),
-        _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, scale, workspace.data_ptr(), ws_bytes,
-        _stream(dev),
+        _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, q_ld, k_ld, v_ld, gb_ld, int(bool(beta_is_logit)),
+        scale, workspace.data_ptr(), ws_bytes, _stream(dev),
     )
     return o, final_state
 
@@ -350,10 +410,11 @@ def causal_conv1d(x, weight, bias=None, initial_state=None, output_final_state=T
 
     x [B, T, D]; weight [D, W] or [D, 1, W] (tap 0 oldest); bias [D] or None; all one dtype. State rows
     [N, D, state_width] (default W: the serving layer's [N, D, W]; lm.py keeps W-1): the raw inputs before
-    each sequence, oldest first. Returns (y [B, T, D], new state [N, D, state_width] or None); ``final_state``
-    may name the tensor to write, ``initial_state`` itself included."""
-    _on_gpu("x", x)
-    dev = x.device
+    each sequence, oldest first. Returns (y [B, T, D] dense, new state [N, D, state_width] or None);
+    ``final_state`` may name the tensor to write, ``initial_state`` itself included. x may be a column slice of
+    wider rows (the q|k|v columns of the input projection), read in place."""
+    dev = x.device if isinstance(x, torch.Tensor) else None
+    x, x_ld = _rows_in_place("x", x, 1, dev)
     _require(x.dim() == 3, f"x: expected [B, T, D], got {tuple(x.shape)}")
     B, T, D = x.shape
     if weight.dim() == 3:
@@ -387,25 +448,27 @@ def causal_conv1d(x, weight, bias=None, initial_state=None, output_final_state=T
                      f"{name}: expected {x.dtype} [{n_seqs}, {D}, {sw}], got {t.dtype} {tuple(t.shape)}")
     if final_state is None and output_final_state:
         final_state = torch.empty(n_seqs, D, sw, device=dev, dtype=x.dtype)
-    y = torch.empty_like(x)
+    y = torch.empty(B, T, D, device=dev, dtype=x.dtype)
     _native.call(
         "zgdn_causal_conv1d_fwd", x.data_ptr(), weight.data_ptr(), _ptr(bias), _code(x, "x"), _ptr(initial_state),
         _ptr(final_state), sw, y.data_ptr(), _ptr(cu_seqlens), _ptr(chunk_indices), n_seqs, n_chunks, B, T, D, W,
-        1 if activation in ("silu", "swish") else 0, _stream(dev),
+        1 if activation in ("silu", "swish") else 0, x_ld, _stream(dev),
     )
     return y, final_state
 
 
 def l2norm(x, eps=1e-6, out_dtype=None):
     """x * rsqrt(sum x^2 + eps) over the last dim (<= 1024); returns (y in ``out_dtype`` (default x's),
-    rstd float32 [...]) -- lm.py:570-571 / FLA l2norm_fwd (gdn.py:416-417)."""
-    _on_gpu("x", x)
+    rstd float32 [...]) -- lm.py:570-571 / FLA l2norm_fwd (gdn.py:416-417). x may be a column slice of wider
+    rows whose dims after the first are dense (q or k of the conv output, [T, H, D]), read in place; y is
+    dense."""
+    x, group, ld = _head_rows("x", x)
     D = x.shape[-1]
     rows = x.numel() // D if D else 0
     y = torch.empty(x.shape, device=x.device, dtype=x.dtype if out_dtype is None else out_dtype)
     rstd = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
     _native.call("zgdn_l2norm_fwd", x.data_ptr(), _code(x, "x"), y.data_ptr(), _code(y, "y"), rstd.data_ptr(),
-                 rows, D, float(eps), _stream(x.device))
+                 rows, D, group, ld, float(eps), _stream(x.device))
     return y, rstd
 
 
@@ -420,17 +483,20 @@ def sigmoid(x, scale=1.0, out_dtype=torch.float32):
 
 def gated_rmsnorm(x, g, weight, eps=1e-5):
     """(rms_norm(x) * weight).to(dtype) * silu(g), product in fp32, over rows of the last dim (<= 1024)
-    (lm.py:584-587 / FLA layer_norm_gated_fwd at gdn.py:435-445). Returns (y, rstd float32 [...])."""
+    (lm.py:584-587 / FLA layer_norm_gated_fwd at gdn.py:435-445). Returns (y, rstd float32 [...]). g may be a
+    column slice of wider rows whose dims after the first are dense (z of the input projection, [T, Hv, V]),
+    read in place."""
     _on_gpu("x", x)
     dev = x.device
     D = x.shape[-1]
-    for name, t in (("g", g), ("weight", weight)):
-        _on_gpu(name, t, dev)
-        _require(t.dtype == x.dtype, f"{name}: dtype {t.dtype}, expected {x.dtype}")
+    _on_gpu("weight", weight, dev)
+    _require(weight.dtype == x.dtype, f"weight: dtype {weight.dtype}, expected {x.dtype}")
+    g, group, g_ld = _head_rows("g", g, dev)
+    _require(g.dtype == x.dtype, f"g: dtype {g.dtype}, expected {x.dtype}")
     _require(g.shape == x.shape and weight.shape == (D,), "gated_rmsnorm: g like x, weight [D]")
     rows = x.numel() // D if D else 0
     y = torch.empty_like(x)
     rstd = torch.empty(x.shape[:-1], device=dev, dtype=torch.float32)
     _native.call("zgdn_gated_rmsnorm_fwd", x.data_ptr(), g.data_ptr(), weight.data_ptr(), _code(x, "x"), y.data_ptr(),
-                 rstd.data_ptr(), rows, D, float(eps), _stream(dev))
+                 rstd.data_ptr(), rows, D, group, g_ld, float(eps), _stream(dev))
     return y, rstd

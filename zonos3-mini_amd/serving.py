@@ -384,6 +384,9 @@ class OriginalGDN:
             keep = valid.view(1, -1, 1)
             a = a.masked_fill(~keep, _MASKED_GATE)
             b = b.masked_fill(~keep, _MASKED_GATE)
+        if self._own_operators() and mixed.dtype == torch.bfloat16:
+            result, conv_final, final = self._run_packed_in_place(x, qkv, z, a, b, cu, chunks, conv, recurrent, mask)
+            return (result, conv_final, final, mixed) if return_mixed else (result, conv_final, final)
         qkv, conv_final = self._conv_fwd(x=qkv.contiguous(), weight=self.conv.weight.squeeze(1), bias=None,
                                          residual=None, initial_state=conv, output_final_state=True,
                                          activation="silu", cu_seqlens=cu, chunk_indices=chunks, BT=CHUNK)
@@ -404,4 +407,32 @@ class OriginalGDN:
             result = self._accent.apply_accent(self.wo, output, result, mask)
         if return_mixed:
             return result, conv_final, final, mixed
+        return result, conv_final, final
+
+    def _own_operators(self) -> bool:
+        return (self._conv_fwd is fla_ops.causal_conv1d_fwd and self._l2norm_fwd is fla_ops.l2norm_fwd
+                and self._beta_fwd is fla_ops.fused_beta_sigmoid_fwd
+                and self._delta_rule_fwd is fla_ops.chunk_gated_delta_rule_fwd
+                and self._norm_fwd is fla_ops.layer_norm_gated_fwd)
+
+    def _run_packed_in_place(self, x, qkv, z, a, b, cu, chunks, conv, recurrent, mask):
+        """``_run_packed``'s operator sequence with this package's operators, the copies left out: the
+        conv reads q|k|v, the chunked kernel a and b (sigmoid(b) taken in the kernel), the gated norm z in
+        place from the projection rows, and the L2 norms and the chunked kernel read q, k, v as column slices
+        of the conv output. Each operator computes what the seam's does (q, k still rounded to bf16 after
+        their norm, as the l2norm operator returns them), so results are bit-identical to the seam route."""
+        y, conv_final = ops.causal_conv1d(qkv, self.conv.weight.squeeze(1), initial_state=conv, activation="silu",
+                                          cu_seqlens=cu, chunk_indices=chunks, state_width=CONV_WIDTH)
+        q, k, v = [t.unflatten(-1, (HEADS, HEAD_DIM)) for t in y.split(HEADS * HEAD_DIM, dim=-1)]
+        q, _ = ops.l2norm(q[0])
+        k, _ = ops.l2norm(k[0])
+        o, final = ops.chunk_fwd(q.unsqueeze(0), k.unsqueeze(0), v, a, b, beta_is_logit=True, scale=HEAD_DIM**-0.5,
+                                 initial_state=recurrent.float(), cu_seqlens=cu, chunk_indices=chunks,
+                                 A_log=self.A_log.float(), dt_bias=self.dt_bias.float())
+        output, _ = ops.gated_rmsnorm(o[0], z[0].unflatten(-1, (HEADS, HEAD_DIM)),
+                                      self.out_weight.to(o.dtype), eps=NORM_EPS)
+        output = output.reshape(x.shape[0], HEADS * HEAD_DIM)
+        result = F.linear(output, self.wo.weight)
+        if mask is not None:
+            result = self._accent.apply_accent(self.wo, output, result, mask)
         return result, conv_final, final
