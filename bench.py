@@ -50,7 +50,7 @@ def _args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres", "layer"], default=None,
                    help="run one workload only (profiling runs); the JSON line then carries that workload")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
@@ -292,6 +292,7 @@ def bench_attnres(torch, gdn):
 
 
 SERVING = dict(hidden=1024, prompt=100, batch_sizes=(2, 32))
+LAYER_T = (4096, 1024)  # prompt lengths of the layer-level prefill line
 
 
 def _window_replay_step(torch, layer, x, slots, rows, cu, chunks):
@@ -380,6 +381,63 @@ def bench_serving(torch, n_steps=200):
             **results}
 
 
+def bench_layer_prefill(torch, reps=20):
+    """The layer drop-in (Zonos3LM._gdn on the HIP kernels, zonos3-mini_amd/layer.py) prefilling a prompt at
+    the release shapes: hidden 1024, 4 heads x 128, conv 1536 x 4, bf16 random weights, zero start states
+    (a fresh cache per call), in_proj and wo GEMMs (hipBLASLt through torch) included."""
+    from types import SimpleNamespace
+
+    import torch.nn.functional as F
+
+    layer = importlib.import_module("zonos3-mini_amd.layer")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1007)
+    bf, hid, heads, hd = torch.bfloat16, 1024, 4, 128
+    inner = heads * hd
+    att = SimpleNamespace(
+        in_proj=SimpleNamespace(weight=(0.02 * torch.randn(4 * inner + 2 * heads, hid, generator=g, device=dev)).to(bf)),
+        conv=SimpleNamespace(weight=(0.2 * torch.randn(3 * inner, 1, 4, generator=g, device=dev)).to(bf)),
+        out_weight=(1 + 0.1 * torch.randn(hd, generator=g, device=dev)).to(bf),
+        A_log=0.2 * torch.randn(heads, generator=g, device=dev), dt_bias=0.2 * torch.randn(heads, generator=g, device=dev),
+        wo=SimpleNamespace(weight=(0.02 * torch.randn(hid, inner, generator=g, device=dev)).to(bf)))
+    model = SimpleNamespace(layers=[SimpleNamespace(attention=att)], _capture=None,
+                            _lin=lambda name, x, w, b=None: F.linear(x, w, b))
+    layer.patch(model)
+    out = {}
+    stream = torch.cuda.Stream(dev)
+    for T in LAYER_T:
+        x = torch.randn(T, hid, generator=g, device=dev).to(bf)
+
+        def call():
+            return model._gdn(x, 0, SimpleNamespace(gdn_state={}, conv_state={}))
+
+        timings = {}
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                call()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                call()
+            for name, fn in (("graph", graph.replay), ("eager", call)):
+                fn()
+                torch.cuda.synchronize()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for _ in range(reps):
+                    fn()
+                end.record(stream)
+                torch.cuda.synchronize()
+                timings[name] = start.elapsed_time(end) / reps * 1e3
+        us = timings["graph"]
+        out[f"T{T}"] = {"us_per_call": round(us, 2), "tokens_per_s": round(T / us * 1e6, 1),
+                        "eager_us_per_call": round(timings["eager"], 2)}
+    return {"workload": "layer drop-in (_gdn) prefill of one prompt at the release shapes: hidden 1024, 4 heads "
+                        "x 128, bf16, zero start states, in_proj and wo GEMMs included; us_per_call: one call per "
+                        "HIP graph replay (GPU time), eager_us_per_call: plain Python calls (host-bound at "
+                        "short prompts)", **out}
+
+
 def calibrate_copy(torch):
     """10 device copies of 64 MiB (torch's copy kernel): the known-size reference for HBM byte counters."""
     dev = torch.device("cuda:0")
@@ -450,6 +508,9 @@ def main():
     if a.only == "attnres":
         print(json.dumps({"workload_only": a.only, **bench_attnres(torch, gdn)}), flush=True)
         return
+    if a.only == "layer":
+        print(json.dumps({"workload_only": a.only, **bench_layer_prefill(torch)}), flush=True)
+        return
     dec = bench_decode(torch, gdn, a.steps, a.warmup)
     line = {
         "metric": METRIC,
@@ -489,6 +550,7 @@ def main():
     line["fused_decode_block"] = bench_fused(torch, gdn)
     line["serving_decode"] = bench_serving(torch)
     line["attnres_route"] = bench_attnres(torch, gdn)
+    line["layer_prefill"] = bench_layer_prefill(torch)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
         line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)

@@ -612,6 +612,31 @@ struct StateArgs {
   int c0, bos, len, nchunks, Hv, h, vb;
 };
 
+// Stores one O wave's outputs of chunk ci: rows t0 .. t0+3 (D layout) of value column vb * VB + j. Lanes l and
+// l ^ 1 (adjacent columns) swap two values by DPP so that each stores two rows as column pairs, 4-byte words
+// (8 for fp32) instead of 2-byte ones, with no per-row condition in full chunks.
+template <typename TOut>
+__device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci, int t0, int j, const float* ov) {
+  const bool odd = (lane_id() & 1) != 0;
+  const float r0 = dpp<DPP_QUAD_XOR1>(odd ? ov[0] : ov[2]), r1 = dpp<DPP_QUAD_XOR1>(odd ? ov[1] : ov[3]);
+  // even lane (column j): rows t0, t0+1 as (own, partner); odd lane (column j): rows t0+2, t0+3 as (partner, own)
+  const float a0 = odd ? r0 : ov[0], b0 = odd ? ov[2] : r0, a1 = odd ? r1 : ov[1], b1 = odd ? ov[3] : r1;
+  const int tr = t0 + (odd ? 2 : 0), tlen = min(CH, a.len - ci * CH);
+  TOut* p = o + ((size_t)(a.bos + ci * CH + tr) * a.Hv + a.h) * DV + a.vb * VB + (j & ~1);
+  const size_t row = (size_t)a.Hv * DV;
+  auto pair = [](TOut* q, float u, float v) {
+    if constexpr (sizeof(TOut) == 2) *reinterpret_cast<uint32_t*>(q) = pack_bf16x2(u, v);
+    else *reinterpret_cast<float2*>(q) = make_float2(u, v);
+  };
+  if (tlen == CH) {
+    pair(p, a0, b0);
+    pair(p + row, a1, b1);
+  } else {
+    if (tr < tlen) pair(p, a0, b0);
+    if (tr + 1 < tlen) pair(p + row, a1, b1);
+  }
+}
+
 // The chunk loop of one wave. URole: waves 0-3 form U' = Ub' - W' S^T of their 16 tokens; the O role
 // (waves 4-7) forms the outputs O = Ob + Q' S^T of their 16 tokens. Both run the same barriers and each
 // wave updates 16 columns of the state slice.
@@ -658,10 +683,15 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     fetch1(wn, nxt);
     lds_barrier();
 
-    // [W'; Q'] S^T for this wave's 16 tokens
-    f32x4 x = zero4();
+    // [W'; Q'] S^T for this wave's 16 tokens, as two independent MFMA chains (half the dependent latency)
+    f32x4 x0 = zero4(), x1 = zero4();
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) x = mfma(cur.A[kk], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk), x);
+    for (int kk = 0; kk < 4; kk += 2) {
+      x0 = mfma(cur.A[kk], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk), x0);
+      x1 = mfma(cur.A[kk + 1], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk + 32), x1);
+    }
+    const f32x4 x = x0 + x1;
+    float ov[4];  // O role: this wave's outputs
     if constexpr (URole) {
       // U' = Ub' - W' S^T as hi + lo bf16
       const float ub[4] = {__uint_as_float(cur.X.x), __uint_as_float(cur.X.y), __uint_as_float(cur.X.z),
@@ -675,35 +705,32 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
       *reinterpret_cast<uint2*>(&sh.UhT[j][t0]) = make_uint2(h01, h23);
       *reinterpret_cast<uint2*>(&sh.UlT[j][t0]) = make_uint2(l01, l23);
     } else {
-      // O = Ob + Q' S^T
+      // O = Ob + Q' S^T (stored after the state update is issued)
       const float ob[4] = {__uint_as_float(cur.X.x << 16), __uint_as_float(cur.X.x & 0xffff0000u),
                            __uint_as_float(cur.X.y << 16), __uint_as_float(cur.X.y & 0xffff0000u)};
-      const int tlen = min(CH, a.len - ci * CH);
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int t = t0 + i4;
-        if (t < tlen)
-          io<TOut>::store(o + ((size_t)(a.bos + ci * CH + t) * a.Hv + a.h) * DV + a.vb * VB + j, ob[i4] + x[i4]);
-      }
+      for (int i4 = 0; i4 < 4; ++i4) ov[i4] = ob[i4] + x[i4];
     }
     fetch2(wn, nxt);
     fetch3(wn, nxt);
     lds_barrier();
 
-    // S <- exp(G_L) S + U'^T K for this wave's 16 columns
-    f32x4 acc = S * __expf(cur.GL);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      acc = mfma(frag(&sh.UhT[0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
-      acc = mfma(frag(&sh.UlT[0][0], LDC, 0, 32 * kk), cur.KT[kk], acc);
-    }
-    S = acc;
+    // S <- exp(G_L) S + U'^T K for this wave's 16 columns (two chains over the key steps)
+    f32x4 acc0 = S * __expf(cur.GL), acc1 = zero4();
+    acc0 = mfma(frag(&sh.UhT[0][0], LDC, 0, 0), cur.KT[0], acc0);
+    acc1 = mfma(frag(&sh.UhT[0][0], LDC, 0, 32), cur.KT[1], acc1);
+    acc0 = mfma(frag(&sh.UlT[0][0], LDC, 0, 0), cur.KT[0], acc0);
+    acc1 = mfma(frag(&sh.UlT[0][0], LDC, 0, 32), cur.KT[1], acc1);
+    S = acc0 + acc1;
+    if constexpr (!URole) store_o_tile(o, a, ci, t0, j, ov);
   };
 
   // two register buffers, alternately filled one chunk ahead (no copies between them). The fetches are
   // unconditional (the last chunk is fetched again at the end) so every path issues the same loads, and the
   // first chunk is peeled so that the loop is entered with the same loads in flight as at its back edge
-  // (which keeps the compiler's wait counts at the loop head from covering the prefetch).
+  // (which keeps the compiler's wait counts at the loop head from covering the prefetch). (Fetching two
+  // chunks ahead, with a third buffer, measured no faster: the loop is bound by the per-CU load rate, not by
+  // memory latency.)
   if (a.nchunks <= 0) return;
   const int last = a.nchunks - 1;
   Pre b0, b1;
