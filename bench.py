@@ -50,7 +50,7 @@ def _args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres", "layer"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres", "layer", "accent"], default=None,
                    help="run one workload only (profiling runs); the JSON line then carries that workload")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
@@ -293,6 +293,7 @@ def bench_attnres(torch, gdn):
 
 SERVING = dict(hidden=1024, prompt=100, batch_sizes=(2, 32))
 LAYER_T = (4096, 1024)  # prompt lengths of the layer-level prefill line
+ACCENT = dict(rows=4096, **{"in": 1024}, out=2056, K=64)
 
 
 def _window_replay_step(torch, layer, x, slots, rows, cu, chunks):
@@ -438,6 +439,47 @@ def bench_layer_prefill(torch, reps=20):
                         "short prompts)", **out}
 
 
+def bench_accent(torch, reps=50):
+    """The accent adapter shift on the mixer's in_proj output (4096 rows, 1024 -> 2056, K = 64 adapter
+    columns, bf16), in place on the projection: the kernel pair against the reference's torch sequence
+    (two GEMMs, a product and a sum, accent.py:37, 62)."""
+    gdn = importlib.import_module("zonos3-mini_amd")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1008)
+    rows, n_in, n_out, K = ACCENT["rows"], ACCENT["in"], ACCENT["out"], ACCENT["K"]
+    bf = torch.bfloat16
+    x = torch.randn(rows, n_in, generator=g, device=dev).to(bf)
+    down = (torch.randn(K, n_in, generator=g, device=dev) / n_in**0.5).to(bf)
+    up = (torch.randn(K, n_out, generator=g, device=dev) / K**0.5).to(bf)
+    mask = (torch.rand(rows, K, generator=g, device=dev) < 0.5).to(bf)
+    y = torch.randn(rows, n_out, generator=g, device=dev).to(bf)
+    stream = torch.cuda.Stream(dev)
+    timings = {}
+    for name, fn in (("kernel", lambda: gdn.ops.accent_shift(x, down, up, mask, y=y, out=y)),
+                     ("torch", lambda: y + ((x @ down.T) * mask) @ up)):
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            torch.cuda._sleep(20_000_000)  # keep the host ahead of the timed launches
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                fn()
+            end.record(stream)
+        torch.cuda.synchronize()
+        timings[name] = start.elapsed_time(end) / reps * 1e3
+    nbytes = 2 * (rows * n_in + 2 * rows * n_out + rows * K + K * (n_in + n_out))
+    gbs = nbytes / timings["kernel"] / 1e3
+    return {"workload": f"accent shift y += ((x @ down.T) * mask) @ up on the in_proj output: {rows} rows, "
+                        f"{n_in} -> {n_out}, K={K}, bf16, in place",
+            "us": round(timings["kernel"], 2), "torch_us": round(timings["torch"], 2),
+            "speedup": round(timings["torch"] / timings["kernel"], 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                         "kernel": "accent_down_bf16_kernel<4> + accent_up_bf16_kernel<true,true>"}}
+
+
 def calibrate_copy(torch):
     """10 device copies of 64 MiB (torch's copy kernel): the known-size reference for HBM byte counters."""
     dev = torch.device("cuda:0")
@@ -511,6 +553,9 @@ def main():
     if a.only == "layer":
         print(json.dumps({"workload_only": a.only, **bench_layer_prefill(torch)}), flush=True)
         return
+    if a.only == "accent":
+        print(json.dumps({"workload_only": a.only, **bench_accent(torch)}), flush=True)
+        return
     dec = bench_decode(torch, gdn, a.steps, a.warmup)
     line = {
         "metric": METRIC,
@@ -551,6 +596,7 @@ def main():
     line["serving_decode"] = bench_serving(torch)
     line["attnres_route"] = bench_attnres(torch, gdn)
     line["layer_prefill"] = bench_layer_prefill(torch)
+    line["accent_shift"] = bench_accent(torch)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(torch)
         line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)

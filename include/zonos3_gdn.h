@@ -186,6 +186,30 @@ int zgdn_sigmoid_fwd(const void* x, int x_dtype, void* y, int y_dtype, size_t n,
 int zgdn_gated_rmsnorm_fwd(const void* x, const void* g, const void* weight, int dtype, void* y, float* rstd,
                            int rows, int D, int g_group, long g_ld, float eps, void* stream);
 
+/*
+ * Bytes of workspace zgdn_accent_shift needs: (rows + out) x K rounded up to 32 bf16 elements (bf16), rows x K
+ * rounded up to 32 floats (fp32).
+ */
+size_t zgdn_accent_workspace_size(int rows, int out, int K, int dtype);
+
+/*
+ * Accent adapter shift of a projection output, y_out = y_in + ((x . down^T) * mask) . up per row: replaces
+ * accent_shift / apply_accent of servers/sgl/src/zonos3_sgl/layers/accent.py:25-62 as the GDN mixer applies
+ * them to in_proj and wo (servers/sgl/src/zonos3_sgl/models/gdn.py:400-401, 448-449).
+ *   x [rows, in] (rows x_ld elements apart), down [K, in], up [K, out], mask [rows, K] (rows mask_ld apart),
+ *   y_in / y_out [rows, out] (rows y_in_ld / y_out_ld apart; y_out may equal y_in; y_in NULL = zeros, i.e.
+ *   the shift alone): all of element type `dtype`. K <= 256 (the summed ranks of the loaded adapters).
+ *   bf16: the reference's rounding points (x . down^T, times mask, . up, the sum with y each rounded to bf16,
+ *   products accumulated in fp32); in, out and x_ld multiples of 8, x, down, up 16-byte aligned. fp32: fp32.
+ *   Each row is computed independently in a fixed order: a row's bits do not depend on the rest of the call
+ *   (the batch invariance accent.py gets from fixed-size row blocks). A zero mask row leaves y exact.
+ *   workspace: device memory (16-byte aligned) of at least zgdn_accent_workspace_size(rows, out, K, dtype)
+ *   bytes.
+ */
+int zgdn_accent_shift(const void* x, long x_ld, const void* down, const void* up, const void* mask, long mask_ld,
+                      const void* y_in, long y_in_ld, void* y_out, long y_out_ld, int rows, int in, int out, int K,
+                      int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

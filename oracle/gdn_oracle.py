@@ -20,6 +20,12 @@ torch restatement and a float64 one (``attnres_route_np``); its pins are closed 
 it, a zero query averages the sources, a dominant logit selects its source, order of sources is
 irrelevant) and the float64 statement.
 
+The accent adapter shift of the mixer's projections (``accent_shift``, ``layers/accent.py:25-62``) has a
+torch restatement and a float64 one (``accent_shift_np``); pins: a zero mask leaves y unchanged, one-hot
+factors move a scaled input column to an output column, adapters on disjoint columns add, and a constant
+mask row equals the merged weight ``W + alpha * up_a^T down_a`` (the "base + alpha * adapter" merge of
+``models/accent_adapters.py:5-8``).
+
 Conventions (all from the reference):
   q, k   [.., T, Hk, K]       v [.., T, Hv, V]       g (log decay), beta [.., T, Hv]
   state  [N, Hv, V, K] float32, value-major (FLA ``state_v_first=True``; lm.py:577, gdn.py:427)
@@ -45,6 +51,10 @@ __all__ = [
     "gated_rmsnorm",
     "gdn_layer",
     "fused_decode_step",
+    "attnres_route",
+    "attnres_route_np",
+    "accent_shift",
+    "accent_shift_np",
     "recurrence_np",
     "chunked_np",
     "make_inputs",
@@ -255,6 +265,20 @@ def attnres_route_np(sources, query, eps) -> np.ndarray:
     w = np.exp(logits - logits.max(0, keepdims=True))
     w /= w.sum(0, keepdims=True)
     return (bank * w[..., None]).sum(0)
+
+
+def accent_shift(x, down, up, mask, y=None):
+    """The accent adapter shift of a projection output, ``servers/sgl/src/zonos3_sgl/layers/accent.py:37``
+    (``((x @ down.T) * mask) @ up``, same ops in the inputs' dtype), added to ``y`` as ``apply_accent`` does
+    (``accent.py:62``) when ``y`` is given."""
+    shift = ((x @ down.T) * mask) @ up
+    return shift if y is None else y + shift
+
+
+def accent_shift_np(x, down, up, mask, y=None) -> np.ndarray:
+    """The same equation in float64 with no intermediate rounding (an independent statement)."""
+    shift = ((_f64(x) @ _f64(down).T) * _f64(mask)) @ _f64(up)
+    return shift if y is None else _f64(y) + shift
 
 
 # ---------------------------------------------------------------------------- float64 statements (numpy)

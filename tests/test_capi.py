@@ -23,7 +23,8 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
-            "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route"} == _declared()
+            "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route", "zgdn_accent_workspace_size",
+            "zgdn_accent_shift"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -117,6 +118,18 @@ def test_bad_arguments_fail_with_a_message(gdn):
     srcs[1] = None
     assert lib.zgdn_attnres_route(srcs, 2, 4, 1024, 1024, 1, p, 1e-5, p, None) == native.EINVAL
     assert b"null source 1" in lib.zgdn_last_error()
+    # accent shift: x, x_ld, down, up, mask, mask_ld, y_in, y_in_ld, y_out, y_out_ld, rows, in, out, K, dtype,
+    # workspace, bytes, stream (no call below passes validation, so none launches)
+    assert lib.zgdn_accent_workspace_size(100, 2056, 40, 1) == (100 + 2056) * 64 * 2
+    assert lib.zgdn_accent_workspace_size(100, 2056, 40, 0) == 100 * 64 * 4
+    acc = [p, 1024, p, p, p, 64, p, 2056, p, 2056, 100, 1024, 2056, 64, 1, p, 0, None]
+    assert lib.zgdn_accent_shift(*acc) == native.EINVAL and b"workspace" in lib.zgdn_last_error()
+    acc[13] = 300
+    assert lib.zgdn_accent_shift(*acc) == native.EUNSUPPORTED and b"K=300" in lib.zgdn_last_error()
+    acc[13], acc[12] = 64, 2052
+    assert lib.zgdn_accent_shift(*acc) == native.EINVAL and b"multiples of 8" in lib.zgdn_last_error()
+    acc[12], acc[5] = 2056, 32
+    assert lib.zgdn_accent_shift(*acc) == native.EINVAL and b"row strides" in lib.zgdn_last_error()
 
 
 def test_host_validation_refuses_cpu_tensors(gdn):

@@ -318,3 +318,41 @@ def test_attnres_route_closed_forms():
     assert rel_err(O.attnres_route(srcs, q, 1e-5), O.attnres_route_np(srcs, q, 1e-5)) < 1e-6
     # a stacked bank is the same as the list
     assert torch.equal(O.attnres_route(torch.stack(srcs), q, 1e-5), O.attnres_route(srcs, q, 1e-5))
+
+
+def test_accent_shift_pins():
+    """The accent shift restatement (layers/accent.py:37, 62) against what the mathematics fixes."""
+    gen = torch.Generator().manual_seed(93)
+    rows, n_in, n_out, ranks = 6, 48, 40, (4, 8)
+    K = sum(ranks)
+    x = torch.randn(rows, n_in, generator=gen)
+    W = torch.randn(n_out, n_in, generator=gen)
+    down, up = torch.randn(K, n_in, generator=gen), torch.randn(K, n_out, generator=gen)
+    y = x @ W.T
+    # a zero mask row leaves y exactly as it was
+    assert torch.equal(O.accent_shift(x, down, up, torch.zeros(rows, K), y), y)
+    # one-hot factors: adapter column k reads input i and writes 2 x its masked value to output j
+    d1, u1 = torch.zeros(K, n_in), torch.zeros(K, n_out)
+    d1[3, 7], u1[3, 11] = 1.0, 2.0
+    m = torch.zeros(rows, K)
+    m[:, 3] = torch.arange(rows, dtype=torch.float32) - 2.0
+    want = torch.zeros(rows, n_out)
+    want[:, 11] = 2.0 * m[:, 3] * x[:, 7]
+    assert torch.equal(O.accent_shift(x, d1, u1, m), want)
+    # a constant mask row alpha on adapter a's columns is the merged weight W + alpha * up_a^T down_a
+    alpha = torch.tensor([0.5, -1.25, 0.0, 2.0, 1.0, 0.75], dtype=torch.float64)
+    cols = slice(ranks[0], K)  # the second adapter
+    mask = torch.zeros(rows, K, dtype=torch.float64)
+    mask[:, cols] = alpha[:, None]
+    merged = np.stack([O._f64(x[r]) @ (O._f64(W) + alpha[r].item() * O._f64(up[cols]).T @ O._f64(down[cols])).T
+                       for r in range(rows)])
+    got = O.accent_shift_np(x, down, up, mask.numpy(), O._f64(x) @ O._f64(W).T)
+    assert np.abs(got - merged).max() < 1e-9 * np.abs(merged).max()
+    # adapters on disjoint columns add
+    ma, mb = torch.zeros(rows, K), torch.zeros(rows, K)
+    ma[:, : ranks[0]] = torch.rand(rows, 1, generator=gen)
+    mb[:, ranks[0]:] = torch.rand(rows, 1, generator=gen)
+    both = O.accent_shift_np(x, down, up, (ma + mb).numpy())
+    assert np.abs(both - O.accent_shift_np(x, down, up, ma.numpy()) - O.accent_shift_np(x, down, up, mb.numpy())).max() < 1e-9
+    # the torch restatement (fp32) agrees with the float64 statement
+    assert rel_err(O.accent_shift(x, down, up, ma + mb, y), O.accent_shift_np(x, down, up, ma + mb, y)) < 1e-5

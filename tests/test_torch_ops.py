@@ -11,7 +11,7 @@ from gdn_testing import announce
 from oracle import gdn_oracle as O
 
 OPS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step", "attnres_route",
-       "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
+       "accent_shift", "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
 
 
 def test_registered_with_mutation_annotations(gdn):
@@ -65,6 +65,10 @@ def test_fake_shapes(gdn):
         bank = [torch.empty(9, 1024, dtype=torch.bfloat16) for _ in range(5)]
         r = z.attnres_route(bank, torch.empty(1024, dtype=torch.bfloat16), 1e-5)
         assert r.shape == (9, 1024) and r.dtype == torch.bfloat16
+        xa = torch.empty(7, 1024, dtype=torch.bfloat16)
+        sh = z.accent_shift(xa, torch.empty(24, 1024, dtype=torch.bfloat16), torch.empty(24, 2056, dtype=torch.bfloat16),
+                            torch.empty(7, 24, dtype=torch.bfloat16))
+        assert sh.shape == (7, 2056) and sh.dtype == torch.bfloat16
         xc = torch.empty(1, 130, 96)
         y, fin = z.causal_conv1d(xc, torch.empty(96, 4), None, None, cu, None, "silu", 3)
         assert y.shape == xc.shape and fin.shape == (3, 96, 3)

@@ -60,6 +60,11 @@ SIGNATURES: dict[str, tuple] = {
     "zgdn_l2norm_fwd": (c_int, [_P, c_int, _P, c_int, _P, c_int, c_int, c_int, c_long, c_float, _P]),
     "zgdn_sigmoid_fwd": (c_int, [_P, c_int, _P, c_int, c_size_t, c_float, _P]),
     "zgdn_gated_rmsnorm_fwd": (c_int, [_P, _P, _P, c_int, _P, _P, c_int, c_int, c_int, c_long, c_float, _P]),
+    "zgdn_accent_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "zgdn_accent_shift": (
+        c_int,
+        [_P, c_long, _P, _P, _P, c_long, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int, c_int, _P, c_size_t, _P],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -500,3 +500,46 @@ def gated_rmsnorm(x, g, weight, eps=1e-5):
     _native.call("zgdn_gated_rmsnorm_fwd", x.data_ptr(), g.data_ptr(), weight.data_ptr(), _code(x, "x"), y.data_ptr(),
                  rstd.data_ptr(), rows, D, group, g_ld, float(eps), _stream(dev))
     return y, rstd
+
+
+def accent_shift(x, down, up, mask, y=None, out=None):
+    """Accent adapter shift of a projection output: ``y + ((x @ down.T) * mask) @ up`` per row
+    (``servers/sgl/src/zonos3_sgl/layers/accent.py:25-62``), the bf16 roundings of those torch ops kept.
+
+    x [rows, in]; down [K, in], up [K, out] (an op's ``_accent``); mask [rows, K]; y [rows, out] or None (the
+    shift alone); all one dtype, K <= 256. x, mask and y may be column slices of wider rows. ``out``: the tensor
+    to write ([rows, out]; may be ``y`` for an in-place update), else a new one. Rows are independent: a row's
+    result does not depend on the other rows of the call."""
+    dev = x.device if isinstance(x, torch.Tensor) else None
+    bf = isinstance(x, torch.Tensor) and x.dtype == torch.bfloat16
+    x, x_ld = _rows_in_place("x", x, 1, dev, 8 if bf else 1, 16 if bf else 1)
+    _require(x.dim() == 2, f"x: expected [rows, in], got {tuple(x.shape)}")
+    rows, n_in = x.shape
+    code = _code(x, "x")
+    for name, t in (("down", down), ("up", up)):
+        _on_gpu(name, t, dev)
+        _require(t.dtype == x.dtype, f"{name}: dtype {t.dtype}, expected {x.dtype}")
+    _require(down.dim() == 2 and down.shape[1] == n_in, f"down: expected [K, {n_in}], got {tuple(down.shape)}")
+    K = down.shape[0]
+    _require(up.dim() == 2 and up.shape[0] == K, f"up: expected [{K}, out], got {tuple(up.shape)}")
+    n_out = up.shape[1]
+    mask, mask_ld = _rows_in_place("mask", mask, 1, dev)
+    _require(mask.dtype == x.dtype and tuple(mask.shape) == (rows, K),
+             f"mask: expected {x.dtype} [{rows}, {K}], got {mask.dtype} {tuple(mask.shape)}")
+    y_ld = 0
+    if y is not None:
+        y, y_ld = _rows_in_place("y", y, 1, dev)
+        _require(y.dtype == x.dtype and tuple(y.shape) == (rows, n_out),
+                 f"y: expected {x.dtype} [{rows}, {n_out}], got {y.dtype} {tuple(y.shape)}")
+    if out is None:
+        out = torch.empty(rows, n_out, device=dev, dtype=x.dtype)
+    _require(isinstance(out, torch.Tensor) and out.is_cuda and out.device == dev and out.dtype == x.dtype
+             and tuple(out.shape) == (rows, n_out), f"out: expected {x.dtype} [{rows}, {n_out}] on {dev}")
+    out_ld = _row_stride(out, 1)
+    _require(out_ld is not None, "out: rows must be contiguous")
+    ws_bytes = int(_native.lib().zgdn_accent_workspace_size(rows, n_out, K, code))
+    workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    _native.call("zgdn_accent_shift", x.data_ptr(), x_ld, down.data_ptr(), up.data_ptr(), mask.data_ptr(), mask_ld,
+                 _ptr(y), y_ld, out.data_ptr(), out_ld, rows, n_in, n_out, K, code, workspace.data_ptr(), ws_bytes,
+                 _stream(dev))
+    return out

@@ -14,6 +14,7 @@ state in place declare it in ``mutates_args``.
 | ``zgdn::fused_decode_step`` | lm.py:563-587 for one new row per stream, conv cache and state in place |
 | ``zgdn::serving_decode_step`` | the serving layer's static decode (gdn.py:329-355) on per-slot caches in place |
 | ``zgdn::attnres_route`` | ``full_attnres_route`` (lm.py:384-389; zonos3.py:99-113) |
+| ``zgdn::accent_shift`` | ``accent_shift`` / ``apply_accent`` (layers/accent.py:25-62) |
 | ``zgdn::causal_conv1d`` | FLA ``causal_conv1d_fwd`` (gdn.py:403-414); lm.py:563-568 |
 | ``zgdn::l2norm`` | FLA ``l2norm_fwd`` (gdn.py:416-417); lm.py:570-571 |
 | ``zgdn::sigmoid`` | FLA ``fused_beta_sigmoid_fwd`` (gdn.py:423); lm.py:573 |
@@ -133,6 +134,16 @@ def _(sources, query, eps):
     return sources[0].new_empty(sources[0].shape)
 
 
+@torch.library.custom_op(f"{NS}::accent_shift", mutates_args=())
+def accent_shift(x: Tensor, down: Tensor, up: Tensor, mask: Tensor, y: Optional[Tensor] = None) -> Tensor:
+    return ops.accent_shift(x, down, up, mask, y=y)
+
+
+@accent_shift.register_fake
+def _(x, down, up, mask, y=None):
+    return x.new_empty(x.shape[0], up.shape[1])
+
+
 # --------------------------------------------------------------------------------------------- row ops
 
 
@@ -184,4 +195,4 @@ def _(x, g, weight, eps=1e-5):
 
 
 OPERATORS = ("recurrent_fwd", "decode_step", "chunk_fwd", "fused_decode_step", "serving_decode_step",
-             "attnres_route", "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
+             "attnres_route", "accent_shift", "causal_conv1d", "l2norm", "sigmoid", "gated_rmsnorm")
