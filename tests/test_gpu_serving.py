@@ -18,7 +18,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from gdn_testing import announce, rel_err
+from gdn_testing import announce, max_abs, rel_err
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -251,3 +251,81 @@ def test_in_place_route_equals_the_operator_seam(serving, cuda):
         torch.cuda.synchronize()
         for name, a, b in zip(("out", "conv", "state", "mixed"), fast, seam):
             assert torch.equal(a, b), (name, keep is None)
+
+
+def test_accent_requests_equal_merged_weights(serving, cuda):
+    """Requests on accent adapters (in_proj / wo shifts through accent hooks on the HIP kernel) through eager
+    prefill, eager decode, static decode (the fused fast path) and an eager extend that replays a tail: each
+    request's rows and live state equal those of a twin layer serving it alone with the merged weights
+    W + alpha * up_a^T down_a -- the "base + alpha * adapter" a request is served as
+    (servers/sgl/src/zonos3_sgl/models/accent_adapters.py:5-8). A request without an accent matches the base
+    weights. Tolerance: 3e-2 relative (max-abs / max) on outputs, 2e-2 on states (bf16 roundings differ
+    between the shifted and the merged products)."""
+    announce("serving mixer with accent adapters vs merged-weight twins")
+    accent = importlib.import_module("zonos3-mini_amd.accent")
+    gen = torch.Generator().manual_seed(4601)
+    w = _weights(4600, torch.bfloat16)
+    K, ranks = 24, (8, 16)
+    fac = {}
+    for name, (n_in, n_out) in (("in_proj", (HIDDEN, 2056)), ("wo", (512, HIDDEN))):
+        fac[name] = ((0.05 * torch.randn(K, n_in, generator=gen)).to(torch.bfloat16),
+                     (0.05 * torch.randn(K, n_out, generator=gen)).to(torch.bfloat16))
+    # request slot -> (adapter columns, strength); slot 2 has no accent
+    plan = {0: (slice(0, ranks[0]), 0.9), 1: (slice(ranks[0], K), 1.4), 2: (None, 0.0)}
+    layer_a = _Driver(serving, w, cuda)
+    for name in ("in_proj", "wo"):
+        getattr(layer_a.layer, name)._accent = tuple(t.to(cuda) for t in fac[name])
+    current = {}
+    layer_a.layer._accent = accent.AccentHooks(lambda: current.get("mask"))
+    twins = {}
+    for s, (cols, alpha) in plan.items():
+        wm = dict(w)
+        if cols is not None:
+            for name in ("in_proj", "wo"):
+                down, up = (t.double() for t in fac[name])
+                wm[name] = (w[name].double() + alpha * up[cols].T @ down[cols]).to(torch.bfloat16)
+        twins[s] = _Driver(serving, wm, cuda)
+    for d in (layer_a, *twins.values()):
+        d.graph_slots = torch.zeros(3, dtype=torch.long, device=cuda)
+        d.layer.enable_graph_decode(d.graph_slots, serving.OriginalGDN.static_tables(cuda, [1, 3]))
+
+    def step(slots, lengths, decode, static=False):
+        x = torch.randn(sum(lengths), HIDDEN, generator=gen).to(torch.bfloat16).to(cuda)
+        rows = []
+        for s, n in zip(slots, lengths):
+            cols, alpha = plan[s]
+            m = torch.zeros(n, K)
+            if cols is not None:
+                m[:, cols] = alpha
+            rows.append(m)
+        current["mask"] = torch.cat(rows).to(torch.bfloat16).to(cuda)
+        outs = []
+        for d, which in [(layer_a, slots)] + [(twins[s], [s]) for s in slots]:
+            picked = [slots.index(s) for s in which]
+            lens = [lengths[i] for i in picked]
+            xs = torch.cat([x[sum(lengths[:i]):sum(lengths[:i]) + lengths[i]] for i in picked])
+            reqs = d._advance(which, lens)
+            d.batch.is_decode, d.batch.gdn_prefill, d.batch.padded_size = decode, None, len(which)
+            d.batch.reqs = d.batch.padded_reqs = reqs
+            if static:
+                d.graph_slots[: len(which)] = torch.tensor(which, device=cuda)
+                d.layer.set_static_mode(True)
+            outs.append(d.layer.forward(xs))
+            if static:
+                d.layer.set_static_mode(False)
+                d.layer.note_graph_forward(reqs)
+        torch.cuda.synchronize()
+        at = 0
+        for i, s in enumerate(slots):
+            got, ref = outs[0][at:at + lengths[i]].float().cpu(), outs[1 + i].float().cpu()
+            assert max_abs(got, ref) < 3e-2 * max(1e-3, float(ref.abs().max())), (s, lengths, decode, static)
+            at += lengths[i]
+
+    step([0, 1, 2], [70, 5, 63], False)  # eager prefill: one request crosses a chunk
+    step([0, 1, 2], [1, 1, 1], True)
+    step([0, 1, 2], [1, 1, 1], True)
+    for _ in range(3):
+        step([0, 1, 2], [1, 1, 1], True, static=True)
+    step([1, 0], [60, 2], False)  # extends replay the tails the decode steps left
+    for s in plan:
+        assert rel_err(layer_a.layer._live_state[s].cpu(), twins[s].layer._live_state[s].cpu()) < 2e-2, s
