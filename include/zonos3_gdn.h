@@ -60,6 +60,16 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
 
 /*
+ * Extra workspace bytes (after zgdn_chunk_workspace_size's) with which zgdn_chunk_fwd runs an unpacked batch of
+ * B sequences of T tokens as segments, 0 when it would not. When the sequential state pass would hold at most
+ * half the current device's CUs (few sequences and heads) and the sequences are long enough for it to pay
+ * (about 48 chunks at one sequence of 4 heads), each sequence is cut into 2 .. 8 segments run at once -- from
+ * zero states, and from the identity to obtain each segment's state map -- and their outputs and states are
+ * combined (the same results up to rounding). A smaller workspace runs the plain pass.
+ */
+size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv);
+
+/*
  * Chunked (WY/UT form, 64-token chunks) gated delta rule over whole sequences on bf16 MFMA with fp32
  * accumulation: the prefill core. Replaces FLA's chunk_gated_delta_rule_fwd as called at
  * servers/sgl/src/zonos3_sgl/models/gdn.py:418-434 (state_v_first=True, chunk_size=64, output o and the
@@ -77,7 +87,8 @@ size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
  *   cu_seqlens [n_seqs+1] + chunk_indices [n_chunks, 2] (sequence, chunk within it; the table of
  *   gdn.py:49-59) for packed sequences (B == 1); otherwise n_chunks is derived from B and T.
  *   initial_state NULL = zeros; final_state NULL = not written; may equal initial_state (in place).
- *   workspace: device memory of at least zgdn_chunk_workspace_size(n_chunks, Hv) bytes.
+ *   workspace: device memory of at least zgdn_chunk_workspace_size(n_chunks, Hv) bytes (plus
+ *   zgdn_chunk_segment_workspace_size(B, T, Hv) for the segmented pass of unpacked batches).
  */
 int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g, const void* beta,
                    int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,

@@ -24,7 +24,7 @@ def test_header_declares_entry_points():
     assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
             "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route", "zgdn_accent_workspace_size",
-            "zgdn_accent_shift"} == _declared()
+            "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -36,6 +36,21 @@ def test_library_exports_every_declared_symbol(gdn):
         assert hasattr(lib, name), name
     assert set(native.SIGNATURES) == _declared()
     assert lib.zgdn_abi_version() == native.ABI_VERSION == 2
+
+
+def test_segment_workspace_follows_the_plan(gdn):
+    """Sizing of the segmented state pass (no device: 256 CUs assumed). Short prompts, many heads or many
+    sequences take the plain pass (no extra bytes); one 4096-token sequence of 4 heads runs 4 segments: Q'P^T
+    (bf16, a token and head) plus, a head, 4 local end states (fp32), 3 maps (bf16 hi and lo) and 3 segment
+    start states (bf16)."""
+    from importlib import import_module
+
+    lib = import_module("zonos3-mini_amd._native").lib()
+    f = lib.zgdn_chunk_segment_workspace_size
+    assert f(1, 1024, 4) == 0 and f(1, 2048, 4) == 0 and f(1, 4096, 16) == 0 and f(8, 4096, 4) == 0
+    hs = 128 * 128
+    assert f(1, 4096, 4) == 4096 * 4 * 128 * 2 + 4 * hs * (4 * 4 + 4 * 3 + 2 * 3)
+    assert f(1, 3072, 4) > 0 and f(2, 4096, 4) > 0
 
 
 def _rec_args(**over):

@@ -138,3 +138,47 @@ def test_rows_read_in_place_and_beta_logits(gdn, cuda, packed):
                                                 v[bi:bi + 1, lo:hi].float().cpu(), g_log[bi:bi + 1, lo:hi],
                                                 beta.cpu()[bi:bi + 1, lo:hi], None, s0[i:i + 1].cpu())
         _check(o1[bi:bi + 1, lo:hi].cpu(), s1[i:i + 1].cpu(), o_ref, s_ref)
+
+
+def _plain_pass(gdn, cuda, q, k, v, g, beta, s0, fin):
+    """zgdn_chunk_fwd with only the phase-1 workspace: the plain (unsegmented) state pass."""
+    native = gdn._native
+    B, T, Hk, _ = q.shape
+    Hv = v.shape[2]
+    nch = B * (-(-T // 64))
+    ws_bytes = int(native.lib().zgdn_chunk_workspace_size(nch, Hv))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=cuda)
+    o = torch.empty(B, T, Hv, 128, dtype=torch.bfloat16, device=cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    native.call("zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), native.BF16, g.data_ptr(),
+                beta.data_ptr(), native.F32, None, None, 0, None if s0 is None else s0.data_ptr(), fin.data_ptr(),
+                o.data_ptr(), None, None, B, nch, B, T, Hk, Hv, 128, 128, Hk * 128, Hk * 128, Hv * 128, Hv, 0,
+                128**-0.5, ws.data_ptr(), ws_bytes, stream)
+    return o
+
+
+@pytest.mark.parametrize("B,T,Hk,Hv,with_state", [(1, 4096, 4, 4, True), (2, 2600, 1, 2, True),
+                                                  (1, 3000, 2, 4, False), (1, 4096, 1, 1, True),
+                                                  (1, 8192, 1, 1, False)])
+def test_segmented_state_pass(gdn, cuda, B, T, Hk, Hv, with_state):
+    """Few sequences and heads, long enough: the state pass runs each sequence as segments at once (from zero
+    states and, for the segment maps, from the identity) and combines them -- here 4 segments (the last ones
+    ragged, two sequences, grouped heads), 5 and 8. Against the oracle, against the plain pass (same inputs,
+    phase-1 workspace only), and with the final state written over the initial one."""
+    announce(f"chunk segmented pass B={B} T={T} Hk={Hk} Hv={Hv} state={with_state}")
+    assert int(gdn._native.lib().zgdn_chunk_segment_workspace_size(B, T, Hv)) > 0  # the path is taken
+    d = O.make_inputs(B, T, Hk, Hv, 128, 128, seed=2500 + T + Hv, dtype=torch.bfloat16, state_std=0.02)
+    x = _dev(d, cuda)
+    s0 = x["s0"] if with_state else None
+    o, s = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=s0)
+    fin_plain = torch.empty(B, Hv, 128, 128, device=cuda)
+    o_plain = _plain_pass(gdn, cuda, x["q"], x["k"], x["v"], x["g"], x["beta"], s0, fin_plain)
+    state = x["s0"].clone() if with_state else torch.zeros_like(x["s0"])
+    o2, s2 = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=state, final_state=state)
+    torch.cuda.synchronize()
+    assert s2 is state and torch.equal(o2, o) and torch.equal(s2, s)
+    o_ref, s_ref = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"], None,
+                                            d["s0"] if with_state else None)
+    _check(o.cpu(), s.cpu(), o_ref, s_ref)
+    _check(o_plain.cpu(), fin_plain.cpu(), o_ref, s_ref)
+    assert max_abs(o.cpu(), o_plain.cpu()) < 2e-2 and rel_err(s.cpu(), fin_plain.cpu()) < 1e-3

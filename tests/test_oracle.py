@@ -95,6 +95,29 @@ def test_split_invariance_prefill_then_decode_steps():
     torch.testing.assert_close(s, s_full, rtol=1e-5, atol=1e-5)
 
 
+def test_segments_combine_through_their_state_maps():
+    """The algebra of the segmented state pass, on the oracle: a segment's map M is its run from the identity
+    state with zero values, its local part L the run from zero; the end state is S_start M + L and each output
+    o_local + S_start (M_t q_t), M_t q_t being the identity run's output. Chained over three segments (V = K)
+    against one run over the whole sequence."""
+    T, H, K = 90, 2, 16
+    d = O.make_inputs(1, T, H, H, K, K, seed=77, state_std=0.3)
+    d["g"] = 0.02 * d["g"]  # decays near 0.99 a token, so that the maps carry weight
+    q, k, v, g, beta = (d[n][0] for n in ("q", "k", "v", "g", "beta"))
+    scale = K**-0.5
+    o_full, s_full = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"], None, d["s0"])
+    S = d["s0"][0]
+    eye = torch.eye(K).expand(H, K, K)
+    for lo, hi in ((0, 40), (40, 70), (70, T)):
+        args = (q[lo:hi], k[lo:hi])
+        o_loc, L = O.gated_delta_sequence(*args, v[lo:hi], g[lo:hi].exp(), beta[lo:hi], scale, torch.zeros(H, K, K))
+        o_map, M = O.gated_delta_sequence(*args, torch.zeros_like(v[lo:hi]), g[lo:hi].exp(), beta[lo:hi], scale, eye)
+        o_seg = o_loc + torch.einsum("hvk,thk->thv", S, o_map)
+        assert rel_err(o_seg, o_full[0, lo:hi]) < 1e-5, (lo, hi)
+        S = S @ M + L
+    assert rel_err(S, s_full[0]) < 1e-5
+
+
 def test_grouped_heads_read_key_head_h_div_group():
     """Hv = 2 Hk equals the ungrouped rule on k/q heads repeated (gdn_kernel.py:16-18)."""
     q, k, v, g, b, s0 = _seq(20, 2, 4, 16, 8, seed=6)

@@ -32,6 +32,7 @@ SIGNATURES: dict[str, tuple] = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     ),
     "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
+    "zgdn_chunk_segment_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "zgdn_chunk_fwd": (
         c_int,
         [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int,

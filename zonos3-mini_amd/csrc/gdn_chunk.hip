@@ -29,6 +29,7 @@
 // D: row 4*(lane/16)+i, column lane%16) and v_mfma_f32_16x16x4_f32 (A[lane%16][lane/16], B[lane/16][lane%16])
 // for the fp32 block inverse. The contraction index of the [W'; Q'] S^T pass is taken in a permuted key order
 // (kappa below) so that two 16 x 16 D tiles of W'^T computed in phase 1 are directly one A fragment.
+#include <type_traits>
 #include <algorithm>
 
 #include "gdn_common.h"
@@ -43,6 +44,14 @@ constexpr int CH = 64;    // chunk length
 constexpr int DK = 128;   // key dim
 constexpr int DV = 128;   // value dim
 constexpr int VB = 16;    // value rows per phase-2 workgroup (DV / VB = 8 workgroups per sequence x head)
+
+// x = hi + lo for a pair of floats: hi their bf16 rounding, lo the bf16 rounding of what is left (together
+// about 16 significant bits)
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16x2(a, b);
+  lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
 constexpr int LDQ = DK + 8;  // padded LDS row (bf16) of a 128-wide matrix
 constexpr int LDC = CH + 8;  // padded LDS row (bf16) of a 64-wide matrix
 constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
@@ -610,6 +619,7 @@ struct StateShared {
 struct StateArgs {
   const uint8_t* ws;
   int c0, bos, len, nchunks, Hv, h, vb;
+  float xs;  // 1, or 0 for a transition run (Ub' and Ob taken as zero: the pass then carries S -> S A_c)
 };
 
 // Stores one O wave's outputs of chunk ci: rows t0 .. t0+3 (D layout) of value column vb * VB + j. Lanes l and
@@ -694,8 +704,8 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     float ov[4];  // O role: this wave's outputs
     if constexpr (URole) {
       // U' = Ub' - W' S^T as hi + lo bf16
-      const float ub[4] = {__uint_as_float(cur.X.x), __uint_as_float(cur.X.y), __uint_as_float(cur.X.z),
-                           __uint_as_float(cur.X.w)};
+      const float ub[4] = {a.xs * __uint_as_float(cur.X.x), a.xs * __uint_as_float(cur.X.y),
+                           a.xs * __uint_as_float(cur.X.z), a.xs * __uint_as_float(cur.X.w)};
       float u[4];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) u[i4] = ub[i4] - x[i4];
@@ -706,8 +716,8 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
       *reinterpret_cast<uint2*>(&sh.UlT[j][t0]) = make_uint2(l01, l23);
     } else {
       // O = Ob + Q' S^T (stored after the state update is issued)
-      const float ob[4] = {__uint_as_float(cur.X.x << 16), __uint_as_float(cur.X.x & 0xffff0000u),
-                           __uint_as_float(cur.X.y << 16), __uint_as_float(cur.X.y & 0xffff0000u)};
+      const float ob[4] = {a.xs * __uint_as_float(cur.X.x << 16), a.xs * __uint_as_float(cur.X.x & 0xffff0000u),
+                           a.xs * __uint_as_float(cur.X.y << 16), a.xs * __uint_as_float(cur.X.y & 0xffff0000u)};
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) ov[i4] = ob[i4] + x[i4];
     }
@@ -749,22 +759,40 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   if (ci < a.nchunks) process(ci, b1, chunk_ws(ci), b0);
 }
 
+// Segmented runs of phase 2 (unpacked batches whose pass would hold few CUs): each sequence is cut into G
+// segments of Cs chunks. "Local" runs carry each segment from a zero state (the first from the sequence's
+// initial state) and write its outputs and end state L_g; "transition" runs carry segments 1.. from the
+// identity with Ub' = Ob = 0, so their state is the segment's map P_c = A_1 .. A_c (S -> S A_c per chunk), their
+// end state M_g and their outputs Q'_c P_c^T. The true state entering segment g is S_g = S_{g-1} M_{g-1} +
+// L_{g-1} (S_1 = L_0) and the true outputs are o_local + (Q' P^T) S_g^T: chunk_combine_kernel and
+// chunk_correct_kernel form them. All local and transition workgroups run at once.
+struct SegRun {
+  int G, Cs;               // segments per sequence, chunks per segment (G == 1: plain runs)
+  float* local_final;      // L [n_seqs * G][Hv][V][K]
+  float* trans_final;      // M^T [n_seqs * (G - 1)][Hv] as bf16 hi [K][K] then lo [K][K]
+  uint16_t* trans_out;     // Q' P^T [n_seqs * T][Hv][K] (bf16)
+};
+
 template <typename TOut>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
     const uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out, TOut* __restrict__ o,
-    const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hv) {
+    const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hv, const SegRun seg) {
   // (ws is not __restrict__: that keeps the compiler from sinking the prefetch loads below the LDS
   // barriers, whose asm memory clobber then pins them where they are issued)
   __shared__ StateShared sh;
 
   // XCD-aware order (workgroups go round-robin over the 8 XCDs): ids are taken in groups of 64 = 8 pairs
-  // (sequence, head) x 8 value blocks, with id % 8 = pair % 8, so the 8 workgroups of one pair run on one
-  // XCD at the same time and share its L2 copy of the chunk workspace. The grid is padded to whole groups.
-  const int pairs = n_seqs * Hv;
+  // (run, head) x 8 value blocks, with id % 8 = pair % 8, so the 8 workgroups of one pair run on one XCD at
+  // the same time and share its L2 copy of the chunk workspace. The grid is padded to whole groups.
+  const int n_local = n_seqs * seg.G * Hv, n_trans = n_seqs * (seg.G - 1) * Hv;
   const int id = blockIdx.x;
   const int pair = (id / 64) * 8 + (id % 8), vb = (id % 64) / 8;
-  if (pair >= pairs) return;
-  const int seq = pair / Hv, h = pair % Hv;
+  if (pair >= n_local + n_trans) return;
+  const bool trans = pair >= n_local;
+  const int vp = trans ? pair - n_local : pair;
+  const int h = vp % Hv, run = vp / Hv;  // run: the (sequence, segment) index among local / transition runs
+  const int seq = trans ? run / (seg.G - 1) : run / seg.G;
+  const int sg = trans ? 1 + run % (seg.G - 1) : run % seg.G;
   const int l = lane_id(), wave = threadIdx.x >> 6;
   const int ncol = 16 * wave + (l & 15);
 
@@ -773,35 +801,272 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   a.Hv = Hv;
   a.h = h;
   a.vb = vb;
-  if (cu != nullptr) {
+  a.xs = trans ? 0.f : 1.f;
+  if (cu != nullptr) {  // packed sequences: plain runs only
     a.bos = cu[seq];
     a.len = cu[seq + 1] - a.bos;
     a.c0 = 0;
     for (int s = 0; s < seq; ++s) a.c0 += (cu[s + 1] - cu[s] + CH - 1) / CH;
   } else {
-    a.bos = seq * T;
-    a.len = T;
-    a.c0 = seq * ((T + CH - 1) / CH);
+    const int nct = (T + CH - 1) / CH;
+    a.bos = seq * T + sg * seg.Cs * CH;
+    a.len = min(seg.Cs * CH, T - sg * seg.Cs * CH);
+    a.c0 = seq * nct + sg * seg.Cs;
   }
   // chunks past the workspace (a chunk table shorter than the sequences need) are not read
   a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
 
   // state slice in the D layout of the state update: rows j = 4*(l/16)+i, column ncol
   f32x4 S;
-  const size_t sbase = (((size_t)seq * Hv + h) * DV + vb * VB) * DK;
+  const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;  // within one [V][K] state
+  const size_t hs = (size_t)DV * DK;
+  if (trans) {
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) S[i4] = s_in != nullptr ? s_in[sbase + (size_t)(4 * (l >> 4) + i4) * DK + ncol] : 0.f;
+    for (int i4 = 0; i4 < 4; ++i4) S[i4] = vb * VB + 4 * (l >> 4) + i4 == ncol ? 1.f : 0.f;
+  } else {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      S[i4] = s_in != nullptr && sg == 0 ? s_in[((size_t)seq * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // settle the state loads before the pipelined loop
 
+  TOut* out = trans ? reinterpret_cast<TOut*>(seg.trans_out) : o;
   if (wave < 4)
-    state_loop<true>(sh, a, o, S);
+    state_loop<true>(sh, a, out, S);
   else
-    state_loop<false>(sh, a, o, S);
+    state_loop<false>(sh, a, out, S);
 
-  if (s_out != nullptr) {
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) s_out[sbase + (size_t)(4 * (l >> 4) + i4) * DK + ncol] = S[i4];
+  if (trans) {  // the segment map transposed (M^T[n][k] = M[k][n]), as bf16 hi and lo parts [K][K] each
+    uint16_t* mt = reinterpret_cast<uint16_t*>(seg.trans_final + ((size_t)run * Hv + h) * hs);
+    const size_t off = (size_t)ncol * DK + vb * VB + 4 * (l >> 4);
+    uint32_t h01, l01, h23, l23;
+    split2(S[0], S[1], h01, l01);
+    split2(S[2], S[3], h23, l23);
+    *reinterpret_cast<uint2*>(mt + off) = make_uint2(h01, h23);
+    *reinterpret_cast<uint2*>(mt + hs + off) = make_uint2(l01, l23);
+    return;
   }
+  float* fin = seg.G > 1 ? seg.local_final + ((size_t)run * Hv + h) * hs
+                         : s_out != nullptr ? s_out + ((size_t)seq * Hv + h) * hs : nullptr;
+  if (fin != nullptr) {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) fin[slice + (size_t)i4 * DK] = S[i4];
+  }
+}
+
+// S_g for the segments g >= 1 of one (sequence, head), as bf16 [V][K] for the correction, and the final
+// state: S_1 = L_0, S_{g+1} = S_g M_g + L_g, final = S_{G-1} M_{G-1} + L_{G-1}. Rows of S never mix (M acts
+// from the right), so each workgroup carries 16 rows through the whole chain on its own: 8 workgroups per
+// (sequence, head). Its rows sit in LDS as bf16 hi and lo parts; each of the 4 waves forms 32 columns of the
+// product on bf16 MFMA (S_hi M_hi + S_hi M_lo + S_lo M_hi: about 16 significant bits, the fp32 state's
+// accuracy) with M^T's hi and lo rows, as the state pass stored them, read straight from memory. The chain is
+// bound by those reads (64 KiB a step for every workgroup, about 2 us): each step's are issued during the
+// previous step's products.
+constexpr int CB_ROWS = 16, CB_LDH = DK + 8, CB_LDT = DK + 4;
+
+__global__ __launch_bounds__(256) void chunk_combine_kernel(const float* __restrict__ local_final,
+                                                            const float* __restrict__ trans_final_t,
+                                                            uint16_t* __restrict__ s_start,
+                                                            float* __restrict__ s_out, int Hv, int G) {
+  __shared__ uint16_t Shi[CB_ROWS][CB_LDH], Slo[CB_ROWS][CB_LDH];  // A operands (bf16 hi / lo of S)
+  __shared__ float Tmp[CB_ROWS][CB_LDT];                            // S M_g, fp32
+  const int rb = blockIdx.x % (DV / CB_ROWS), pair = blockIdx.x / (DV / CB_ROWS);
+  const int seq = pair / Hv, h = pair % Hv, r0 = rb * CB_ROWS;
+  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+  const int er = tid >> 4, ec = (tid & 15) * 8;  // this thread's 8 elements of the 16 rows
+  const size_t hs = (size_t)DV * DK;
+  auto L = [&](int g) { return local_final + (((size_t)seq * G + g) * Hv + h) * hs + (size_t)(r0 + er) * DK + ec; };
+  auto MT = [&](int g) {
+    return reinterpret_cast<const uint16_t*>(trans_final_t + (((size_t)seq * (G - 1) + g - 1) * Hv + h) * hs);
+  };
+  const bool want_final = s_out != nullptr;
+  auto needed = [&](int g) { return g < G - 1 || (g == G - 1 && want_final); };  // step g's product
+  // B fragments of column tile t (M^T rows 32 wave + 16 t + l % 16) and key block k (32 k + 8 (l / 16) ..)
+  auto load_b = [&](const uint16_t* mt, int k, uint4* b) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint16_t* p = mt + (size_t)(32 * wave + 16 * t + (l & 15)) * DK + 32 * k + 8 * (l >> 4);
+      b[(t * (DK / 32) + k) * 2] = *reinterpret_cast<const uint4*>(p);
+      b[(t * (DK / 32) + k) * 2 + 1] = *reinterpret_cast<const uint4*>(p + hs);
+    }
+  };
+  auto load_l = [&](int g, float4* v) {
+    v[0] = *reinterpret_cast<const float4*>(L(g));
+    v[1] = *reinterpret_cast<const float4*>(L(g) + 4);
+  };
+  auto put_s = [&](float4 a, float4 b) {  // 8 elements into the hi / lo tiles
+    uint32_t hw[4], lw[4];
+    split2(a.x, a.y, hw[0], lw[0]);
+    split2(a.z, a.w, hw[1], lw[1]);
+    split2(b.x, b.y, hw[2], lw[2]);
+    split2(b.z, b.w, hw[3], lw[3]);
+    *reinterpret_cast<uint4*>(&Shi[er][ec]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *reinterpret_cast<uint4*>(&Slo[er][ec]) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  };
+  constexpr int NB = 2 * (DK / 32) * 2;
+  float4 l0[2], l1[2];
+  uint4 b0[NB], b1[NB];
+  load_l(0, l0);
+  put_s(l0[0], l0[1]);  // S_1 = L_0
+  if (needed(1)) {
+#pragma unroll
+    for (int k = 0; k < DK / 32; ++k) load_b(MT(1), k, b0);
+    load_l(1, l0);
+  }
+  // one step: S_g out as bf16, then S <- S M_g + L_g from (bv, lv); the next step's operands into (bn, ln)
+  auto step = [&](int g, const uint4* bv, const float4* lv, uint4* bn, float4* ln) __attribute__((always_inline)) {
+    const bool pre = needed(g + 1);
+    __syncthreads();  // the hi / lo tiles hold S_g
+    uint16_t* so = s_start + (((size_t)seq * (G - 1) + g - 1) * Hv + h) * hs + (size_t)(r0 + er) * DK + ec;
+    *reinterpret_cast<uint4*>(so) = *reinterpret_cast<const uint4*>(&Shi[er][ec]);  // bf16 S_g = its hi part
+    if (!needed(g)) return;  // the last segment, the final state not wanted
+    if (pre) load_l(g + 1, ln);
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k = 0; k < DK / 32; ++k) {
+      if (pre) load_b(MT(g + 1), k, bn);
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&Shi[l & 15][32 * k + 8 * (l >> 4)]);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(&Slo[l & 15][32 * k + 8 * (l >> 4)]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, bv[(t * (DK / 32) + k) * 2]);
+        const bf16x8 bl = __builtin_bit_cast(bf16x8, bv[(t * (DK / 32) + k) * 2 + 1]);
+        acc[t] = mfma(ah, bh, acc[t]);
+        acc[t] = mfma(ah, bl, acc[t]);
+        acc[t] = mfma(al, bh, acc[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Tmp[4 * (l >> 4) + i][32 * wave + 16 * t + (l & 15)] = acc[t][i];
+    __syncthreads();  // every wave has read the hi / lo tiles and written its columns of S M_g
+    const float4 p0 = *reinterpret_cast<const float4*>(&Tmp[er][ec]);
+    const float4 p1 = *reinterpret_cast<const float4*>(&Tmp[er][ec + 4]);
+    const float4 s0 = make_float4(p0.x + lv[0].x, p0.y + lv[0].y, p0.z + lv[0].z, p0.w + lv[0].w);
+    const float4 s1 = make_float4(p1.x + lv[1].x, p1.y + lv[1].y, p1.z + lv[1].z, p1.w + lv[1].w);
+    if (g == G - 1) {  // the final state, fp32
+      float* fo = s_out + ((size_t)seq * Hv + h) * hs + (size_t)(r0 + er) * DK + ec;
+      *reinterpret_cast<float4*>(fo) = s0;
+      *reinterpret_cast<float4*>(fo + 4) = s1;
+    } else {
+      put_s(s0, s1);
+    }
+  };
+  for (int g = 1; g < G; g += 2) {
+    step(g, b0, l0, b1, l1);
+    if (g + 1 < G) step(g + 1, b1, l1, b0, l0);
+  }
+}
+
+// o[t][h][:] += (Q' P^T)[t][h][:] S_g^T for the rows of one chunk of a segment g >= 1: D = S_g . (Q'P^T)^T on
+// bf16 MFMA with the values as the M side (A = S_g rows, staged once in LDS for the 4 waves) and the tokens as
+// the N side (B = Q'P^T rows), so each lane's D values are 4 adjacent values of one row of o (one 8-byte
+// read-modify-write, its read issued first). 4 waves x 16 tokens.
+constexpr int CR_LD = DK + 8;  // bf16 row stride of the staged S_g: 272 bytes, rows 4 banks apart
+template <typename TOut>
+__global__ __launch_bounds__(256) void chunk_correct_kernel(const uint16_t* __restrict__ s_start,
+                                                            const uint16_t* __restrict__ trans_out,
+                                                            TOut* __restrict__ o, int T, int Hv, int G, int Cs) {
+  __shared__ uint16_t Ssh[DV][CR_LD];
+  using OWord = std::conditional_t<sizeof(TOut) == 2, uint2, float4>;  // 4 outputs
+  const int nseg = G - 1;
+  const int c = blockIdx.x % Cs, h = (blockIdx.x / Cs) % Hv, run = blockIdx.x / (Cs * Hv);
+  const int seq = run / nseg, sg = 1 + run % nseg;
+  const int t0 = sg * Cs * CH + c * CH;  // within the sequence
+  if (t0 >= T) return;                   // the whole workgroup
+  const int len = min(CH, T - t0);
+  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+  const int tok = 16 * wave + (l & 15);
+  const bool live = tok < len;
+  const uint16_t* S = s_start + (((size_t)seq * nseg + sg - 1) * Hv + h) * (size_t)DV * DK;
+  const size_t row0 = (size_t)seq * T + t0;
+  TOut* orow = o + ((row0 + tok) * Hv + h) * DV + 4 * (l >> 4);
+  OWord ow[DV / 16];
+  uint4 bw[DK / 32];
+  if (live) {
+#pragma unroll
+    for (int t = 0; t < DV / 16; ++t) ow[t] = *reinterpret_cast<const OWord*>(orow + 16 * t);
+#pragma unroll
+    for (int kq = 0; kq < DK / 32; ++kq)
+      bw[kq] = *reinterpret_cast<const uint4*>(trans_out + ((row0 + tok) * Hv + h) * DK + 32 * kq + 8 * (l >> 4));
+  } else {
+#pragma unroll
+    for (int kq = 0; kq < DK / 32; ++kq) bw[kq] = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < DV * DK / 8 / 256; ++i) {  // S_g -> LDS, 16 bytes a thread per pass
+    const int e = tid + 256 * i, r = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
+    *reinterpret_cast<uint4*>(&Ssh[r][c8]) = *reinterpret_cast<const uint4*>(S + (size_t)r * DK + c8);
+  }
+  __syncthreads();
+  f32x4 acc[DV / 16];
+#pragma unroll
+  for (int t = 0; t < DV / 16; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kq = 0; kq < DK / 32; ++kq) {
+    const bf16x8 b = __builtin_bit_cast(bf16x8, bw[kq]);
+#pragma unroll
+    for (int t = 0; t < DV / 16; ++t) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ssh[16 * t + (l & 15)][32 * kq + 8 * (l >> 4)]);
+      acc[t] = mfma(a, b, acc[t]);
+    }
+  }
+  if (!live) return;
+#pragma unroll
+  for (int t = 0; t < DV / 16; ++t) {
+    if constexpr (sizeof(TOut) == 2) {
+      const uint2 w = ow[t];
+      const float v0 = __uint_as_float(w.x << 16) + acc[t][0], v1 = __uint_as_float(w.x & 0xffff0000u) + acc[t][1];
+      const float v2 = __uint_as_float(w.y << 16) + acc[t][2], v3 = __uint_as_float(w.y & 0xffff0000u) + acc[t][3];
+      *reinterpret_cast<uint2*>(orow + 16 * t) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+    } else {
+      const float4 w = ow[t];
+      *reinterpret_cast<float4*>(orow + 16 * t) =
+          make_float4(w.x + acc[t][0], w.y + acc[t][1], w.z + acc[t][2], w.w + acc[t][3]);
+    }
+  }
+}
+
+// Segments for an unpacked batch of B sequences of T tokens (G == 1: the plain pass). Costs measured on
+// MI355X at 4 heads, one sequence (graph replay, hundredths of a microsecond): the plain pass 64 a chunk; a
+// segmented one 80 a chunk of a segment, 207 a combine step and 985 fixed (the combine's and the correction's
+// launches and the longer state pass). A segment count in 2 .. 8 is taken when its local and transition
+// workgroups all fit one per CU and it is the cheapest.
+struct SegPlan {
+  int G, Cs;
+};
+SegPlan seg_plan(int B, int T, int Hv, int n_cu) {
+  const int nct = (T + CH - 1) / CH;
+  const long base = (long)B * Hv * (DV / VB);
+  SegPlan p{1, nct};
+  if (2 * base > n_cu) return p;
+  long best = 64L * nct;
+  for (int g = 2; g <= 8; ++g) {
+    const int cs = (nct + g - 1) / g, gg = (nct + cs - 1) / cs;
+    if (cs < 4 || gg < 2 || base * (2 * gg - 1) > n_cu) continue;
+    const long cost = 985 + 80L * cs + 207L * (gg - 1);
+    if (cost < best) {
+      best = cost;
+      p = SegPlan{gg, cs};
+    }
+  }
+  return p;
+}
+
+// Bytes past the phase-1 workspace a segmented run needs: Q'P^T (bf16 [B*T][Hv][K]), L (fp32, G per
+// sequence), M^T (bf16 hi and lo, G - 1 per sequence), S_g (bf16, G - 1 per sequence).
+size_t seg_bytes(int B, int T, int Hv, const SegPlan& p) {
+  if (p.G <= 1) return 0;
+  const size_t hs = (size_t)DV * DK;
+  return (size_t)B * T * Hv * DK * 2 + (size_t)B * Hv * hs * (4 * p.G + 4 * (p.G - 1) + 2 * (p.G - 1));
+}
+
+int device_cus() {
+  int dev = 0, n_cu = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    n_cu = 256;
+  return std::max(1, n_cu);
 }
 
 template <typename TG>
@@ -830,6 +1095,12 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
 
 extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
   return (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0) * zgdn::WS_CHUNK;
+}
+
+extern "C" size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv) {
+  using namespace zgdn;
+  if (B < 1 || T < 1 || Hv < 1) return 0;
+  return seg_bytes(B, T, Hv, seg_plan(B, T, Hv, device_cus()));
 }
 
 extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
@@ -879,8 +1150,34 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
       launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
                               N, T, scale, qk_l2norm, rs, ws, s);
   }
-  dim3 grid2(((N * Hv + 7) / 8) * 64);  // groups of 8 (sequence, head) pairs x DV / VB = 8 value blocks
+  // phase 2: plain runs, or (unpacked batches that would hold few CUs, workspace permitting) segmented runs
+  const SegPlan plan = cu_seqlens == nullptr ? seg_plan(B, T, Hv, device_cus()) : SegPlan{1, 0};
+  const size_t base = zgdn_chunk_workspace_size(n_chunks, Hv);
+  const bool segmented = plan.G > 1 && workspace_bytes >= base + seg_bytes(B, T, Hv, plan);
+  SegRun run{1, (T + CH - 1) / CH, nullptr, nullptr, nullptr};
+  uint16_t* s_start = nullptr;
+  if (segmented) {
+    const size_t hs = (size_t)DV * DK;
+    uint8_t* p = ws + base;
+    run.G = plan.G;
+    run.Cs = plan.Cs;
+    run.trans_out = reinterpret_cast<uint16_t*>(p);
+    p += (size_t)B * T * Hv * DK * 2;
+    run.local_final = reinterpret_cast<float*>(p);
+    p += (size_t)B * plan.G * Hv * hs * 4;
+    run.trans_final = reinterpret_cast<float*>(p);
+    p += (size_t)B * (plan.G - 1) * Hv * hs * 4;
+    s_start = reinterpret_cast<uint16_t*>(p);
+  }
+  const long runs = (long)N * Hv * (2 * run.G - 1);  // local + transition (run, head) pairs
+  dim3 grid2((unsigned)(((runs + 7) / 8) * 64));     // groups of 8 pairs x DV / VB = 8 value blocks
   hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,
-                     (bf16*)o, cu_seqlens, N, n_chunks, T, Hv);
+                     (bf16*)o, cu_seqlens, N, n_chunks, T, Hv, run);
+  if (segmented) {
+    hipLaunchKernelGGL(chunk_combine_kernel, dim3(N * Hv * (DV / CB_ROWS)), dim3(256), 0, s, run.local_final,
+                       run.trans_final, s_start, final_state, Hv, run.G);
+    hipLaunchKernelGGL((chunk_correct_kernel<bf16>), dim3(N * (run.G - 1) * Hv * run.Cs), dim3(256), 0, s, s_start,
+                       run.trans_out, (bf16*)o, T, Hv, run.G, run.Cs);
+  }
   return check_launch(fn);
 }

@@ -246,6 +246,8 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
         final_state = torch.empty(n_seqs, Hv, V, K, device=dev, dtype=torch.float32)
     o = torch.empty(B, T, Hv, V, device=dev, dtype=torch.bfloat16)
     ws_bytes = int(_native.lib().zgdn_chunk_workspace_size(n_chunks, Hv))
+    if cu_seqlens is None:  # room for the segmented state pass when the library would take it
+        ws_bytes += int(_native.lib().zgdn_chunk_segment_workspace_size(B, T, Hv))
     workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     scale = K**-0.5 if scale is None else float(scale)
     _native.call(
