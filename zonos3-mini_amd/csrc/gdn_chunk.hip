@@ -202,6 +202,25 @@ __device__ __forceinline__ f32x4 mm16_f32(const float* A, int ra, int ca, const 
   return acc;
 }
 
+// acc += (A1 - A2)[ra.., ca..] . B[rb.., cb..] (16x16 blocks of swizzled 64x64 fp32 matrices; A2's block at
+// ra2, ca2).
+__device__ __forceinline__ f32x4 mm16_f32_diff(const float* A1, int ra, int ca, const float* A2, int ra2, int ca2,
+                                               const float* B, int rb, int cb, int l, f32x4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const float a = A1[at32<16>(ra + (l & 15), ca + 4 * s + (l >> 4))] - A2[at32<16>(ra2 + (l & 15), ca2 + 4 * s + (l >> 4))];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, B[at32<16>(rb + 4 * s + (l >> 4), cb + (l & 15))], acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// A 16x16 D tile (rows r0 + 4 (lane / 16) + i, column c0 + lane % 16) into a swizzled 64x64 fp32 matrix,
+// negated when asked.
+__device__ __forceinline__ void put16_f32(float* M, int r0, int c0, int l, f32x4 d, bool neg) {
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) M[at32<16>(r0 + 4 * (l >> 4) + i4, c0 + (l & 15))] = neg ? -d[i4] : d[i4];
+}
+
 struct Prep {
   // one 32 KiB region reused by phase: raw q, k rows -> A, T (fp32) -> the bf16 forms of T and R -> Ub^T
   union {
@@ -210,8 +229,8 @@ struct Prep {
       uint16_t Ks[CH * DK];
     } a;
     struct {
-      float As[CH * CH];  // strictly lower A (fp32, 256-byte rows); rows 0-15 above the diagonal blocks hold
-      float Ts[CH * CH];  // the block inverse's per-wave scratch.  T = (I + A)^-1 (fp32)
+      float As[CH * CH];  // strictly lower A (fp32, 256-byte rows), then N_ij = T_ii A_ij in its blocks
+      float Ts[CH * CH];  // T = (I + A)^-1 (fp32); blocks (0, 1..3) hold the inverse's pair products
     } b;
     struct {
       uint16_t TBF[CH * CH];  // diag(Fk) T diag(beta exp(G) rk)   (B operand of W'^T)
@@ -302,6 +321,18 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
     uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
 
+    // gate inputs of the chunk's tokens (wave 7), loaded first so that their latency overlaps the rows'
+    float gi = 0.f, bi = 0.f, alog = 0.f, dtb = 0.f;
+    if (wave == P1_WAVES - 1 && l < cr.len) {
+      const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
+      gi = io<TG>::load(g + gh);
+      bi = io<TG>::load(beta + gh);
+      if constexpr (GATE) {
+        alog = A_log[h];
+        dtb = dt_bias[h];
+      }
+    }
+
     // 1. rows of q, k, v -> LDS (zeros past the chunk end): Q, K row-major, K^T and V^T; gate and G.
     {
       const uint4 z = make_uint4(0, 0, 0, 0);
@@ -326,12 +357,8 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
       store_pair_t(sm.VsT, c8, r0, v0, v1);
     }
     if (wave == P1_WAVES - 1) {
-      float gi = 0.f, bi = 0.f;
       if (l < cr.len) {
-        const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
-        gi = io<TG>::load(g + gh);
-        if constexpr (GATE) gi = -__expf(A_log[h]) * softplus(gi + dt_bias[h]);
-        bi = io<TG>::load(beta + gh);
+        if constexpr (GATE) gi = -__expf(alog) * softplus(gi + dtb);
         if (rs.beta_sigmoid) bi = sigmoid(bi);
       }
 #pragma unroll
@@ -441,22 +468,38 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     }
     __syncthreads();
 
-    // 3b. off-diagonal blocks, one block row per level: T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj (fp32 MFMA);
-    // wave w's scratch Y is the (unused) block (0, w + 1) of As
-    for (int bi = 1; bi < 4; ++bi) {
-      const int bj = wave;
-      if (bj < bi) {
-        f32x4 y = zero4();
-        for (int m = bj; m < bi; ++m) y = mm16_f32(sm.u.b.As, bi * 16, m * 16, sm.u.b.Ts, m * 16, bj * 16, l, y);
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[at32<16>(4 * (l >> 4) + i4, 16 * (wave + 1) + (l & 15))] = y[i4];
-        wave_sync_lds();
-        f32x4 z = mm16_f32(sm.u.b.Ts, bi * 16, bi * 16, sm.u.b.As, 0, 16 * (wave + 1), l, zero4());
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.u.b.Ts[at32<16>(bi * 16 + 4 * (l >> 4) + i4, bj * 16 + (l & 15))] = -z[i4];
-      }
-      __syncthreads();
+    // 3b. off-diagonal blocks. With N_ij = T_ii A_ij (i > j) the block recurrence T_ij = -sum_m N_im T_mj
+    // unrolls to T_10 = -N_10 T_00, T_21 = -N_21 T_11, T_32 = -N_32 T_22, T_20 = (N_21 N_10 - N_20) T_00,
+    // T_31 = (N_32 N_21 - N_31) T_11 and T_30 = (N_32 N_20 - N_30) T_00 + (N_32 N_21 - N_31) T_10: three levels
+    // of 16x16 fp32 MFMA block products (a chain of four instead of nine). N overwrites A's blocks; the pair
+    // products sit in T's (unused) blocks above the diagonal.
+    if (wave < 6) {  // level 1: N_ij, one block a wave
+      const int bi = wave < 1 ? 1 : (wave < 3 ? 2 : 3), bj = wave - bi * (bi - 1) / 2;
+      put16_f32(sm.u.b.As, 16 * bi, 16 * bj, l,
+                mm16_f32(sm.u.b.Ts, 16 * bi, 16 * bi, sm.u.b.As, 16 * bi, 16 * bj, l, zero4()), false);
     }
+    __syncthreads();
+    if (wave < 3) {  // level 2: T_10, T_21, T_32
+      put16_f32(sm.u.b.Ts, 16 * (wave + 1), 16 * wave, l,
+                mm16_f32(sm.u.b.As, 16 * (wave + 1), 16 * wave, sm.u.b.Ts, 16 * wave, 16 * wave, l, zero4()), true);
+    } else if (wave < 6) {  // N_21 N_10 -> T(0,1), N_32 N_20 -> T(0,2), N_32 N_21 -> T(0,3)
+      const int ai = wave == 3 ? 2 : 3, aj = wave == 3 ? 1 : 2, bi = wave == 3 ? 1 : 2, bj = wave == 5 ? 1 : 0;
+      put16_f32(sm.u.b.Ts, 0, 16 * (wave - 2), l,
+                mm16_f32(sm.u.b.As, 16 * ai, 16 * aj, sm.u.b.As, 16 * bi, 16 * bj, l, zero4()), false);
+    }
+    __syncthreads();
+    if (wave < 3) {  // level 3: T_20, T_31, T_30
+      if (wave == 0) {
+        put16_f32(sm.u.b.Ts, 32, 0, l, mm16_f32_diff(sm.u.b.Ts, 0, 16, sm.u.b.As, 32, 0, sm.u.b.Ts, 0, 0, l, zero4()), false);
+      } else if (wave == 1) {
+        put16_f32(sm.u.b.Ts, 48, 16, l, mm16_f32_diff(sm.u.b.Ts, 0, 48, sm.u.b.As, 48, 16, sm.u.b.Ts, 16, 16, l, zero4()), false);
+      } else {
+        f32x4 t = mm16_f32_diff(sm.u.b.Ts, 0, 32, sm.u.b.As, 48, 0, sm.u.b.Ts, 0, 0, l, zero4());
+        t = mm16_f32_diff(sm.u.b.Ts, 0, 48, sm.u.b.As, 48, 16, sm.u.b.Ts, 16, 0, l, t);
+        put16_f32(sm.u.b.Ts, 48, 0, l, t, false);
+      }
+    }
+    __syncthreads();
 
     // 3c. the bf16 forms of T, in 2x2 blocks (through registers: they overwrite A and T): TBF = diag(Fk) T
     // diag(Bk), TBT = (T diag(Bk))^T, LB = (T - I) diag(beta). (T above the diagonal blocks is masked.)
