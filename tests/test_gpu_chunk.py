@@ -182,3 +182,40 @@ def test_segmented_state_pass(gdn, cuda, B, T, Hk, Hv, with_state):
     _check(o.cpu(), s.cpu(), o_ref, s_ref)
     _check(o_plain.cpu(), fin_plain.cpu(), o_ref, s_ref)
     assert max_abs(o.cpu(), o_plain.cpu()) < 2e-2 and rel_err(s.cpu(), fin_plain.cpu()) < 1e-3
+
+
+@pytest.mark.parametrize("B,T,Hk,Hv,gate,with_state", [(1, 4096, 16, 16, False, False),
+                                                       (2, 1000, 4, 8, True, True),
+                                                       (4, 700, 8, 8, False, True),
+                                                       (1, 192, 8, 8, True, False),
+                                                       (1, 100, 16, 16, False, True)])
+def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_state):
+    """Unpacked batches of 8 .. 32 (sequence, head) chains take the overlapped launch (phase 1 and the state
+    pass in one kernel, linked by per-chunk ready flags on each XCD). It runs the same arithmetic as the two
+    launches, so the results are bit-identical to them (ZGDN_CHUNK_OVERLAP=0), on two calls in a row (the
+    control block is reset per call), and within tolerance of the oracle. Shapes: the prefill workload, two
+    sequences with grouped heads and a ragged last chunk, the largest (32 chains) and smallest (8) batches,
+    and a sequence shorter than two chunks."""
+    announce(f"chunk overlapped B={B} T={T} Hk={Hk} Hv={Hv} gate={gate} state={with_state}")
+    gen = torch.Generator().manual_seed(2600 + T + Hv)
+    d = O.make_inputs(B, T, Hk, Hv, 128, 128, seed=2600 + B + T, dtype=torch.bfloat16, state_std=0.02)
+    x = _dev(d, cuda)
+    s0 = x["s0"] if with_state else None
+    kw = {}
+    g_in, g_log = x["g"], d["g"]
+    if gate:
+        a = torch.randn(B, T, Hv, generator=gen)
+        A_log, dt_bias = 0.3 * torch.randn(Hv, generator=gen), 0.3 * torch.randn(Hv, generator=gen)
+        kw = dict(A_log=A_log.to(cuda), dt_bias=dt_bias.to(cuda))
+        g_in, g_log = a.to(cuda), -A_log.exp() * F.softplus(a + dt_bias)
+    runs = []
+    for overlap in ("1", "1", "0"):
+        monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
+        runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], g_in, x["beta"], initial_state=s0, **kw))
+    torch.cuda.synchronize()
+    (o1, s1), (o2, s2), (o0, s0_) = runs
+    assert torch.equal(o1, o0) and torch.equal(s1, s0_)
+    assert torch.equal(o2, o0) and torch.equal(s2, s0_)
+    o_ref, s_ref = O.gated_delta_recurrence(d["q"], d["k"], d["v"], g_log, d["beta"], None,
+                                            d["s0"] if with_state else None)
+    _check(o1.cpu(), s1.cpu(), o_ref, s_ref)

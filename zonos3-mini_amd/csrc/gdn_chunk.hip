@@ -31,6 +31,7 @@
 // (kappa below) so that two 16 x 16 D tiles of W'^T computed in phase 1 are directly one A fragment.
 #include <type_traits>
 #include <algorithm>
+#include <cstdlib>
 
 #include "gdn_common.h"
 
@@ -296,19 +297,17 @@ struct RowStrides {
   int beta_sigmoid;
 };
 
-// Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
-// Two workgroups share a CU, so one's loads and barriers overlap the other's work.
+// One phase-1 item (chunk x head, item = chunk * Hv + head): W', Q', K^T, Ub', Ob and G_L of the chunk into its
+// workspace. Ends with a workgroup barrier (the LDS may be reused at once).
 template <typename TG, bool GATE>
-__global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
+__device__ __forceinline__ void prep_item(Prep& sm, int item,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
     int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
     uint8_t* __restrict__ ws) {
-  __shared__ Prep sm;
   const int wave = threadIdx.x >> 6;
-
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  {
     // thread indices made opaque per item: the swizzled LDS addresses derived from them are then formed
     // where they are used instead of being hoisted out of the loop and kept live (or spilled) throughout
     int tz = 0;
@@ -636,6 +635,21 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
   }
 }
 
+// Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
+// Two workgroups share a CU, so one's loads and barriers overlap the other's work.
+template <typename TG, bool GATE>
+__global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
+    int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
+    uint8_t* __restrict__ ws) {
+  __shared__ Prep sm;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x)
+    prep_item<TG, GATE>(sm, item, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, n_items, T, Hk, Hv,
+                        scale, qk_l2norm, rs, ws);
+}
+
 // ----------------------------------------------------------------------------------------------- phase 2
 
 constexpr int P2_WAVES = 8;
@@ -663,7 +677,19 @@ struct StateArgs {
   const uint8_t* ws;
   int c0, bos, len, nchunks, Hv, h, vb;
   float xs;  // 1, or 0 for a transition run (Ub' and Ob taken as zero: the pass then carries S -> S A_c)
+  // overlapped form: the ready flag of item (chunk c, head h) is flags[c * Hv + h], nonzero once phase 1
+  // has stored the item; err is set when a wait gives up
+  int* flags;
+  int* err;
 };
+
+// Bound on a state pass's wait for one item (a few tenths of a second): a wait that runs out records an error,
+// and the wave then waits no more, so that every wave of the kernel ends soon.
+constexpr int SPIN_MAX = 1 << 17;
+
+__device__ __forceinline__ int load_flag(const int* f) {
+  return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Stores one O wave's outputs of chunk ci: rows t0 .. t0+3 (D layout) of value column vb * VB + j. Lanes l and
 // l ^ 1 (adjacent columns) swap two values by DPP so that each stores two rows as column pairs, 4-byte words
@@ -693,7 +719,7 @@ __device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci
 // The chunk loop of one wave. URole: waves 0-3 form U' = Ub' - W' S^T of their 16 tokens; the O role
 // (waves 4-7) forms the outputs O = Ob + Q' S^T of their 16 tokens. Both run the same barriers and each
 // wave updates 16 columns of the state slice.
-template <bool URole, typename TOut>
+template <bool URole, typename TOut, bool Wait>
 __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, TOut* o, f32x4& S) {
   const int l = lane_id(), wave = threadIdx.x >> 6;
   const int tb = wave & 3;               // this wave's token tile
@@ -730,9 +756,35 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     x.KT[1] = ld16(w, offK + 1024u);
   };
 
-  auto process = [&](int ci, const Pre& cur, const uint8_t* wn, Pre& nxt) {
+  // Overlapped form: before the loads of chunk ni, wait for its ready flag (read one chunk ahead, so that
+  // the flag's round trip is hidden when phase 1 is ahead) and issue the read of the next one's.
+  if (a.nchunks <= 0) return;
+  const int last = a.nchunks - 1;
+  const int* fbase = Wait ? a.flags + (size_t)a.c0 * a.Hv + a.h : nullptr;
+  int fl = 0;
+  bool gave_up = false;
+  auto wait_ready = [&](int ni) {
+    if constexpr (Wait) {
+      int f = gave_up ? 1 : fl;
+      for (int n = 0; f == 0; ++n) {
+        if (n == SPIN_MAX) {
+          if (l == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          gave_up = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        f = load_flag(fbase + (size_t)ni * a.Hv);
+      }
+      asm volatile("" ::: "memory");  // the chunk's loads stay behind the wait
+      fl = load_flag(fbase + (size_t)min(ni + 1, last) * a.Hv);
+    }
+  };
+
+  auto process = [&](int ci, const Pre& cur, int ni, Pre& nxt) {
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) sh.Ss[4 * (l >> 4) + i4][pcol] = f32_to_bf16(S[i4]);
+    wait_ready(ni);
+    const uint8_t* wn = chunk_ws(ni);
     fetch1(wn, nxt);
     lds_barrier();
 
@@ -784,22 +836,22 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   // (which keeps the compiler's wait counts at the loop head from covering the prefetch). (Fetching two
   // chunks ahead, with a third buffer, measured no faster: the loop is bound by the per-CU load rate, not by
   // memory latency.)
-  if (a.nchunks <= 0) return;
-  const int last = a.nchunks - 1;
   Pre b0, b1;
   {
+    if constexpr (Wait) fl = load_flag(fbase);
+    wait_ready(0);
     const uint8_t* w0 = chunk_ws(0);
     fetch1(w0, b0);
     fetch2(w0, b0);
     fetch3(w0, b0);
   }
-  process(0, b0, chunk_ws(min(1, last)), b1);
+  process(0, b0, min(1, last), b1);
   int ci = 1;
   for (; ci + 1 < a.nchunks; ci += 2) {
-    process(ci, b1, chunk_ws(ci + 1), b0);
-    process(ci + 1, b0, chunk_ws(min(ci + 2, last)), b1);
+    process(ci, b1, ci + 1, b0);
+    process(ci + 1, b0, min(ci + 2, last), b1);
   }
-  if (ci < a.nchunks) process(ci, b1, chunk_ws(ci), b0);
+  if (ci < a.nchunks) process(ci, b1, ci, b0);
 }
 
 // Segmented runs of phase 2 (unpacked batches whose pass would hold few CUs): each sequence is cut into G
@@ -874,10 +926,12 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // settle the state loads before the pipelined loop
 
   TOut* out = trans ? reinterpret_cast<TOut*>(seg.trans_out) : o;
+  a.flags = nullptr;
+  a.err = nullptr;
   if (wave < 4)
-    state_loop<true>(sh, a, out, S);
+    state_loop<true, TOut, false>(sh, a, out, S);
   else
-    state_loop<false>(sh, a, out, S);
+    state_loop<false, TOut, false>(sh, a, out, S);
 
   if (trans) {  // the segment map transposed (M^T[n][k] = M[k][n]), as bf16 hi and lo parts [K][K] each
     uint16_t* mt = reinterpret_cast<uint16_t*>(seg.trans_final + ((size_t)run * Hv + h) * hs);
@@ -894,6 +948,123 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   if (fin != nullptr) {
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) fin[slice + (size_t)i4 * DK] = S[i4];
+  }
+}
+
+// ------------------------------------------------------------------------------- phases 1 and 2 overlapped
+//
+// One launch for unpacked batches whose state pass holds few CUs (8 .. 32 (sequence, head) chains at 8 XCDs):
+// the state pass of a chain starts once phase 1 has stored the chain's first chunk and then trails it, instead
+// of waiting for every item of every chain. Phase 1 alone fills the chip; the plain state pass holds one CU per
+// 16 value rows of each chain and is bound by the rate at which those CUs take the workspace in, so run after
+// each other the two add up while side by side most of phase 1 hides under the state pass.
+//
+// Producer and consumers of a chunk's workspace must share one L2: the XCDs' L2 caches are not coherent with
+// each other, and the fences that would make them so write back or drop a whole L2. So every chain belongs to
+// one queue, chain % n_q, and a workgroup serves the queue of the XCD it runs on (the hardware XCC_ID register).
+// On queue q the first workgroups to arrive take items (as many as the queue has chains), the next ones the
+// state jobs (chain x 8 value blocks, one each), the rest items again; item workgroups take the queue's items
+// in chunk order from a second counter until none are left. An item's workgroup stores the item, waits for
+// its stores to reach the L2 and sets the item's ready flag; a state job reads each chunk's flag (one chunk
+// ahead) before its loads. No data of a chunk is in any L1 before its flag is set (only state jobs read the
+// workspace, and only after the flag), so plain loads see the stores through the shared L2.
+// Progress: items never wait, and the items a state job waits for are taken by running workgroups of its queue
+// as long as a queue's resident workgroups outnumber its state jobs (at most 32 of the 64 that two per CU give an
+// XCD); a wait that runs out (SPIN_MAX) records an error and the kernel still ends.
+// The control block (per-queue ticket counters, the error word, one flag per item) is zeroed before each launch.
+constexpr int FQ_MAX = 8;          // queues (one per XCD)
+constexpr int FQ_MAX_CHAINS = 4;   // chains per queue: 32 state workgroups of the 64 resident on an XCD
+
+struct FusedCtl {
+  int* tickets;  // role ticket of queue q at [64 q], its item ticket at [64 q + 32] (own 128-byte lines)
+  int* err;
+  int* flags;    // [n_items]
+  int n_q;       // queues in use (XCDs of the device)
+};
+
+size_t fused_ctl_bytes(int n_items) { return 256 * (FQ_MAX + 1) + (((size_t)n_items * 4 + 255) / 256) * 256; }
+
+__global__ void zero_ints_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+union FusedShared {
+  Prep p;
+  StateShared s;
+};
+
+template <typename TG, bool GATE>
+__global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, int B, int T, int Hk, int Hv, float scale, int qk_l2norm,
+    const RowStrides rs, uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out,
+    bf16* __restrict__ o, const FusedCtl ctl) {
+  __shared__ FusedShared sm;
+  __shared__ int tk;
+  int xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+  const int qi = xcc % ctl.n_q;
+  const int nct = (T + CH - 1) / CH, n_chains = B * Hv;
+  const int nch = (n_chains - qi + ctl.n_q - 1) / ctl.n_q;  // chains of this queue: qi + n_q m, m < nch
+  const int n_state = nch * (DV / VB);
+
+  // role: the first nch workgroups to arrive on the queue take items, the next n_state the state jobs, the
+  // rest items again
+  if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 64 * qi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int role = tk;
+  if (role >= nch && role < nch + n_state) {
+    const int js = role - nch, ch = qi + ctl.n_q * (js / (DV / VB)), vb = js % (DV / VB);
+    const int b = ch / Hv, h = ch % Hv;
+    const int l = lane_id(), wave = threadIdx.x >> 6;
+    StateArgs a;
+    a.ws = ws;
+    a.Hv = Hv;
+    a.h = h;
+    a.vb = vb;
+    a.xs = 1.f;
+    a.bos = b * T;
+    a.len = T;
+    a.c0 = b * nct;
+    a.nchunks = nct;
+    a.flags = ctl.flags;
+    a.err = ctl.err;
+    const int ncol = 16 * wave + (l & 15);
+    const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
+    const size_t hs = (size_t)DV * DK;
+    f32x4 S;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) S[i4] = s_in != nullptr ? s_in[((size_t)b * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_setprio(3);  // the sequential pass's waves issue ahead of phase-1 waves on their CU
+    if (wave < 4)
+      state_loop<true, bf16, true>(sm.s, a, o, S);
+    else
+      state_loop<false, bf16, true>(sm.s, a, o, S);
+    if (s_out != nullptr) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) s_out[((size_t)b * Hv + h) * hs + slice + (size_t)i4 * DK] = S[i4];
+    }
+    return;
+  }
+
+  // items of the queue in chunk order, u = chunk * nch + m (chain qi + n_q m)
+  const int n_q_items = nch * nct, n_items = B * nct * Hv;
+  for (;;) {
+    __syncthreads();  // every thread has read tk (and the LDS of the last item is free)
+    if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 64 * qi + 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int u = tk;
+    if (u >= n_q_items) break;
+    const int ch = qi + ctl.n_q * (u % nch), c = u / nch;
+    const int b = ch / Hv, h = ch % Hv;
+    const int item = (b * nct + c) * Hv + h;
+    prep_item<TG, GATE>(sm.p, item, q, k, v, g, beta, A_log, dt_bias, nullptr, nullptr, B, n_items, T, Hk, Hv,
+                        scale, qk_l2norm, rs, ws);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(ctl.flags + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1105,6 +1276,13 @@ size_t seg_bytes(int B, int T, int Hv, const SegPlan& p) {
   return (size_t)B * T * Hv * DK * 2 + (size_t)B * Hv * hs * (4 * p.G + 4 * (p.G - 1) + 2 * (p.G - 1));
 }
 
+// The overlapped launch is taken unless the environment sets ZGDN_CHUNK_OVERLAP=0 (read at each call): the
+// two-launch form stays reachable for comparison.
+bool overlap_enabled() {
+  const char* e = std::getenv("ZGDN_CHUNK_OVERLAP");
+  return !(e != nullptr && e[0] == '0');
+}
+
 int device_cus() {
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -1137,7 +1315,8 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
 }  // namespace zgdn
 
 extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
-  return (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0) * zgdn::WS_CHUNK;
+  const size_t items = (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0);
+  return items * zgdn::WS_CHUNK + zgdn::fused_ctl_bytes((int)items);
 }
 
 extern "C" size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv) {
@@ -1185,14 +1364,6 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
   hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = (uint8_t*)workspace;
   const bool gate = A_log != nullptr;
-  if (n_chunks > 0) {
-    if (gb_dtype == ZGDN_F32)
-      launch_prep<float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                               N, T, scale, qk_l2norm, rs, ws, s);
-    else
-      launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
-                              N, T, scale, qk_l2norm, rs, ws, s);
-  }
   // phase 2: plain runs, or (unpacked batches that would hold few CUs, workspace permitting) segmented runs
   const SegPlan plan = cu_seqlens == nullptr ? seg_plan(B, T, Hv, device_cus()) : SegPlan{1, 0};
   const size_t base = zgdn_chunk_workspace_size(n_chunks, Hv);
@@ -1211,6 +1382,46 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
     run.trans_final = reinterpret_cast<float*>(p);
     p += (size_t)B * (plan.G - 1) * Hv * hs * 4;
     s_start = reinterpret_cast<uint16_t*>(p);
+  }
+  // phases 1 and 2 in one overlapped launch: unpacked batches of 8 .. 32 chains on the plain pass
+  const int n_q = std::min(FQ_MAX, std::max(1, device_cus() / 32));  // XCDs (32 CUs each on gfx950)
+  const long n_chains = (long)B * Hv;
+  if (cu_seqlens == nullptr && !segmented && n_chunks > 0 && n_chains >= n_q && n_chains <= (long)FQ_MAX_CHAINS * n_q &&
+      overlap_enabled()) {
+    const int n_items = n_chunks * Hv;
+    int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
+    const FusedCtl ctl{ctl_base, ctl_base + 64 * FQ_MAX, ctl_base + 64 * (FQ_MAX + 1), n_q};
+    const int n_ctl = (int)(fused_ctl_bytes(n_items) / 4);
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((n_ctl + 255) / 256), dim3(256), 0, s, ctl_base, n_ctl);
+    const dim3 grid(P1_WGS_PER_CU * device_cus());
+    if (gb_dtype == ZGDN_F32) {
+      if (gate)
+        hipLaunchKernelGGL((chunk_fused_kernel<float, true>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
+                           (const uint16_t*)k, (const uint16_t*)v, (const float*)g, (const float*)beta, A_log,
+                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+      else
+        hipLaunchKernelGGL((chunk_fused_kernel<float, false>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
+                           (const uint16_t*)k, (const uint16_t*)v, (const float*)g, (const float*)beta, A_log,
+                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+    } else {
+      if (gate)
+        hipLaunchKernelGGL((chunk_fused_kernel<bf16, true>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
+                           (const uint16_t*)k, (const uint16_t*)v, (const bf16*)g, (const bf16*)beta, A_log,
+                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+      else
+        hipLaunchKernelGGL((chunk_fused_kernel<bf16, false>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
+                           (const uint16_t*)k, (const uint16_t*)v, (const bf16*)g, (const bf16*)beta, A_log,
+                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+    }
+    return check_launch(fn);
+  }
+  if (n_chunks > 0) {
+    if (gb_dtype == ZGDN_F32)
+      launch_prep<float>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
+                               N, T, scale, qk_l2norm, rs, ws, s);
+    else
+      launch_prep<bf16>(gate, n_chunks, Hk, Hv, q, k, v, g, beta, A_log, dt_bias, cu_seqlens, chunk_indices,
+                              N, T, scale, qk_l2norm, rs, ws, s);
   }
   const long runs = (long)N * Hv * (2 * run.G - 1);  // local + transition (run, head) pairs
   dim3 grid2((unsigned)(((runs + 7) / 8) * 64));     // groups of 8 pairs x DV / VB = 8 value blocks
