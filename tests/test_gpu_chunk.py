@@ -188,14 +188,15 @@ def test_segmented_state_pass(gdn, cuda, B, T, Hk, Hv, with_state):
                                                        (2, 1000, 4, 8, True, True),
                                                        (4, 700, 8, 8, False, True),
                                                        (1, 192, 8, 8, True, False),
-                                                       (1, 100, 16, 16, False, True)])
+                                                       (1, 100, 16, 16, False, True),
+                                                       (4, 500, 16, 16, True, True)])
 def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_state):
     """Unpacked batches of 8 .. 32 (sequence, head) chains take the overlapped launch (phase 1 and the state
     pass in one kernel, linked by per-chunk ready flags on each XCD). It runs the same arithmetic as the two
     launches, so the results are bit-identical to them (ZGDN_CHUNK_OVERLAP=0), on two calls in a row (the
     control block is reset per call), and within tolerance of the oracle. Shapes: the prefill workload, two
-    sequences with grouped heads and a ragged last chunk, the largest (32 chains) and smallest (8) batches,
-    and a sequence shorter than two chunks."""
+    sequences with grouped heads and a ragged last chunk, the largest (32 chains) and smallest (8) batches of
+    the few-chains order, a sequence shorter than two chunks, and 64 chains (the many-chains order)."""
     announce(f"chunk overlapped B={B} T={T} Hk={Hk} Hv={Hv} gate={gate} state={with_state}")
     gen = torch.Generator().manual_seed(2600 + T + Hv)
     d = O.make_inputs(B, T, Hk, Hv, 128, 128, seed=2600 + B + T, dtype=torch.bfloat16, state_std=0.02)
@@ -219,3 +220,33 @@ def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_stat
     o_ref, s_ref = O.gated_delta_recurrence(d["q"], d["k"], d["v"], g_log, d["beta"], None,
                                             d["s0"] if with_state else None)
     _check(o1.cpu(), s1.cpu(), o_ref, s_ref)
+
+
+@pytest.mark.parametrize("lengths,Hk,Hv", [([64, 1, 130, 0, 70, 200, 63, 128], 2, 4),
+                                          ([700, 64, 1000, 3, 512, 129, 66, 2048, 300, 90, 1, 450], 8, 16),
+                                          ([100] * 40, 4, 8)])
+def test_overlapped_launch_packed(gdn, cuda, monkeypatch, lengths, Hk, Hv):
+    """Packed sequences (and their empty, one-token and ragged members) in the overlapped launch's many-chains
+    order: bit-identical to the two launches, within tolerance of the oracle, initial states carried and the
+    empty sequence's state passed through."""
+    announce(f"chunk overlapped packed n={len(lengths)} Hk={Hk} Hv={Hv}")
+    cu, chunks = O.chunk_tables(lengths)
+    d = O.make_inputs(1, sum(lengths), Hk, Hv, 128, 128, seed=2700 + len(lengths), dtype=torch.bfloat16,
+                      state_std=0.02, n_states=len(lengths))
+    x = _dev(d, cuda)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=cuda)
+    ch_t = torch.tensor(chunks, dtype=torch.int32, device=cuda)
+    runs = []
+    for overlap in ("1", "1", "0"):
+        monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
+        runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t,
+                                  chunk_indices=ch_t))
+    torch.cuda.synchronize()
+    (o1, s1), (o2, s2), (o0, s0_) = runs
+    assert torch.equal(o1, o0) and torch.equal(s1, s0_)
+    assert torch.equal(o2, o0) and torch.equal(s2, s0_)
+    o_ref, s_ref = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"], None, d["s0"], cu_seqlens=cu)
+    _check(o1.cpu(), s1.cpu(), o_ref, s_ref)
+    for i, n in enumerate(lengths):
+        if n == 0:
+            assert torch.equal(s1[i].cpu(), d["s0"][i])

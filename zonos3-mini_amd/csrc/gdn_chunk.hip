@@ -953,36 +953,44 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 
 // ------------------------------------------------------------------------------- phases 1 and 2 overlapped
 //
-// One launch for unpacked batches whose state pass holds few CUs (8 .. 32 (sequence, head) chains at 8 XCDs):
-// the state pass of a chain starts once phase 1 has stored the chain's first chunk and then trails it, instead
-// of waiting for every item of every chain. Phase 1 alone fills the chip; the plain state pass holds one CU per
-// 16 value rows of each chain and is bound by the rate at which those CUs take the workspace in, so run after
-// each other the two add up while side by side most of phase 1 hides under the state pass.
+// One launch in which phase 1 and the state pass run side by side. The state pass of a (sequence, head) chain
+// starts once phase 1 has stored the chain's first chunk and then trails it, instead of waiting for every item
+// of every chain: for few chains (unpacked batches of 8 .. 32 at 8 XCDs) most of phase 1 hides under the
+// state pass, which holds one CU per 16 value rows of each chain; for many chains (packed batches) each
+// chunk's workspace is read back while it is still in the L2 or the last-level cache rather than from HBM.
 //
 // Producer and consumers of a chunk's workspace must share one L2: the XCDs' L2 caches are not coherent with
 // each other, and the fences that would make them so write back or drop a whole L2. So every chain belongs to
-// one queue, chain % n_q, and a workgroup serves the queue of the XCD it runs on (the hardware XCC_ID register).
-// On queue q the first workgroups to arrive take items (as many as the queue has chains), the next ones the
-// state jobs (chain x 8 value blocks, one each), the rest items again; item workgroups take the queue's items
-// in chunk order from a second counter until none are left. An item's workgroup stores the item, waits for
-// its stores to reach the L2 and sets the item's ready flag; a state job reads each chunk's flag (one chunk
-// ahead) before its loads. No data of a chunk is in any L1 before its flag is set (only state jobs read the
-// workspace, and only after the flag), so plain loads see the stores through the shared L2.
-// Progress: items never wait, and the items a state job waits for are taken by running workgroups of its queue
-// as long as a queue's resident workgroups outnumber its state jobs (at most 32 of the 64 that two per CU give an
-// XCD); a wait that runs out (SPIN_MAX) records an error and the kernel still ends.
-// The control block (per-queue ticket counters, the error word, one flag per item) is zeroed before each launch.
-constexpr int FQ_MAX = 8;          // queues (one per XCD)
-constexpr int FQ_MAX_CHAINS = 4;   // chains per queue: 32 state workgroups of the 64 resident on an XCD
+// one queue, chain % n_q, and a workgroup serves the queue of the XCD it runs on (the hardware XCC_ID
+// register). Each workgroup takes one role when it arrives (role ticket of its queue): state worker or item
+// worker. Item workers take the queue's items from an item ticket in a fixed order until none are left; state
+// workers take its state jobs (chain x 8 value blocks, chains in queue order) from a state ticket. An item's
+// workgroup sets the item's ready flag once its workspace stores have reached the L2; a state job reads each
+// chunk's flag (one chunk ahead) before its loads. No data of a chunk is in any L1 before its flag is set (only
+// state jobs read the workspace, and only after the flag), so plain loads see the stores through the shared L2.
+//   few chains (at most FQ_FEW_CHAINS a queue, unpacked): the first nch arrivals take items, the next 8 nch one
+//     state job each, the rest items; items in chunk order across the queue's chains.
+//   many chains: the first arrival takes items, the next FQ_STATE_WORKERS state jobs one after another, the
+//     rest items; items chain after chain, so state jobs start in the order their chains are produced.
+// Progress: items never wait and every queue's first arrival takes items, so every item is stored whatever the
+// number of resident workgroups; a wait that runs out (SPIN_MAX) records an error and the kernel still ends.
+// The control block (per-queue tickets, the error word, one flag per item) is zeroed before each launch.
+constexpr int FQ_MAX = 8;              // queues (one per XCD)
+constexpr int FQ_FEW_CHAINS = 4;       // chains per queue of the few-chains order (32 state workgroups of 64)
+constexpr int FQ_STATE_WORKERS = 24;   // workgroups per queue taking state jobs in the many-chains order
+constexpr int FQ_MAX_SEQS = 256;       // packed sequences (LDS table of chunk offsets)
+constexpr int FQ_MAX_QCHAINS = 512;    // chains per queue in the many-chains order (LDS table)
 
 struct FusedCtl {
-  int* tickets;  // role ticket of queue q at [64 q], its item ticket at [64 q + 32] (own 128-byte lines)
+  int* tickets;  // queue q: role ticket at [96 q], item ticket at [96 q + 32], state ticket at [96 q + 64]
   int* err;
   int* flags;    // [n_items]
   int n_q;       // queues in use (XCDs of the device)
+  int few;       // few-chains order
 };
 
-size_t fused_ctl_bytes(int n_items) { return 256 * (FQ_MAX + 1) + (((size_t)n_items * 4 + 255) / 256) * 256; }
+constexpr size_t FQ_HEADER = 256 * 13;  // tickets (8 queues x 3 lines of 128 bytes), error word
+size_t fused_ctl_bytes(int n_items) { return FQ_HEADER + (((size_t)n_items * 4 + 255) / 256) * 256; }
 
 __global__ void zero_ints_kernel(int* p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
@@ -993,74 +1001,148 @@ union FusedShared {
   StateShared s;
 };
 
+// Exclusive prefix sum over the workgroup's threads (x of thread t at position t): out[t] for t < n, out[n] the
+// total. wsum: 8 ints of LDS.
+__device__ __forceinline__ void block_exclusive_scan(int x, int n, int* out, int* wsum) {
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  int inc = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(inc, d);
+    if (l >= d) inc += y;
+  }
+  if (l == 63) wsum[w] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int i = 0; i < w; ++i) base += wsum[i];
+  if ((int)threadIdx.x < n) out[threadIdx.x] = base + inc - x;
+  if ((int)threadIdx.x == n - 1) out[n] = base + inc;
+  if (n == 0 && threadIdx.x == 0) out[0] = 0;
+  __syncthreads();
+}
+
 template <typename TG, bool GATE>
 __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, int B, int T, int Hk, int Hv, float scale, int qk_l2norm,
-    const RowStrides rs, uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out,
-    bf16* __restrict__ o, const FusedCtl ctl) {
+    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
+    int n_seqs, int n_chunks, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
+    uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out, bf16* __restrict__ o,
+    const FusedCtl ctl) {
   __shared__ FusedShared sm;
   __shared__ int tk;
+  __shared__ int wsum[8];
+  __shared__ int seq_c0[FQ_MAX_SEQS + 1];   // packed: first chunk of each sequence
+  __shared__ int qpref[FQ_MAX_QCHAINS + 1];  // many chains: first item ticket of each chain of the queue
   int xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
   const int qi = xcc % ctl.n_q;
-  const int nct = (T + CH - 1) / CH, n_chains = B * Hv;
+  const int nct_t = (T + CH - 1) / CH;  // unpacked: chunks per sequence
+  const int n_chains = n_seqs * Hv;
   const int nch = (n_chains - qi + ctl.n_q - 1) / ctl.n_q;  // chains of this queue: qi + n_q m, m < nch
   const int n_state = nch * (DV / VB);
+  const int n_items = n_chunks * Hv;
+  auto seq_bos = [&](int sq) { return cu != nullptr ? cu[sq] : sq * T; };
+  auto seq_len = [&](int sq) { return cu != nullptr ? cu[sq + 1] - cu[sq] : T; };
 
-  // role: the first nch workgroups to arrive on the queue take items, the next n_state the state jobs, the
-  // rest items again
-  if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 64 * qi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // tables of the many-chains order
+  if (!ctl.few) {
+    if (cu != nullptr) {
+      const int t = threadIdx.x;
+      block_exclusive_scan(t < n_seqs ? (cu[t + 1] - cu[t] + CH - 1) / CH : 0, n_seqs, seq_c0, wsum);
+    }
+    const int t = threadIdx.x;
+    int len = 0;
+    if (t < nch) {
+      const int sq = (qi + ctl.n_q * t) / Hv;
+      len = (seq_len(sq) + CH - 1) / CH;
+    }
+    block_exclusive_scan(len, nch, qpref, wsum);
+  }
+  auto chunk0 = [&](int sq) { return cu != nullptr ? seq_c0[sq] : sq * nct_t; };
+  const int n_q_items = ctl.few ? nch * nct_t : qpref[nch];
+
+  // role
+  if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 96 * qi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const int role = tk;
-  if (role >= nch && role < nch + n_state) {
-    const int js = role - nch, ch = qi + ctl.n_q * (js / (DV / VB)), vb = js % (DV / VB);
-    const int b = ch / Hv, h = ch % Hv;
+  const int n_first = ctl.few ? nch : 1;
+  const int n_workers = ctl.few ? n_state : min(n_state, FQ_STATE_WORKERS);
+
+  if (role >= n_first && role < n_first + n_workers) {
     const int l = lane_id(), wave = threadIdx.x >> 6;
-    StateArgs a;
-    a.ws = ws;
-    a.Hv = Hv;
-    a.h = h;
-    a.vb = vb;
-    a.xs = 1.f;
-    a.bos = b * T;
-    a.len = T;
-    a.c0 = b * nct;
-    a.nchunks = nct;
-    a.flags = ctl.flags;
-    a.err = ctl.err;
-    const int ncol = 16 * wave + (l & 15);
-    const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
-    const size_t hs = (size_t)DV * DK;
-    f32x4 S;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) S[i4] = s_in != nullptr ? s_in[((size_t)b * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_setprio(3);  // the sequential pass's waves issue ahead of phase-1 waves on their CU
-    if (wave < 4)
-      state_loop<true, bf16, true>(sm.s, a, o, S);
-    else
-      state_loop<false, bf16, true>(sm.s, a, o, S);
-    if (s_out != nullptr) {
+    for (;;) {
+      __syncthreads();  // every thread has read tk (and the LDS of the last job is free)
+      if (threadIdx.x == 0)
+        tk = __hip_atomic_fetch_add(ctl.tickets + 96 * qi + 64, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int js = tk;
+      if (js >= n_state) break;
+      const int ch = qi + ctl.n_q * (js / (DV / VB)), vb = js % (DV / VB);
+      const int sq = ch / Hv, h = ch % Hv;
+      StateArgs a;
+      a.ws = ws;
+      a.Hv = Hv;
+      a.h = h;
+      a.vb = vb;
+      a.xs = 1.f;
+      a.bos = seq_bos(sq);
+      a.len = seq_len(sq);
+      a.c0 = chunk0(sq);
+      a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
+      a.flags = ctl.flags;
+      a.err = ctl.err;
+      const int ncol = 16 * wave + (l & 15);
+      const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
+      const size_t hs = (size_t)DV * DK;
+      f32x4 S;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) s_out[((size_t)b * Hv + h) * hs + slice + (size_t)i4 * DK] = S[i4];
+      for (int i4 = 0; i4 < 4; ++i4)
+        S[i4] = s_in != nullptr ? s_in[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (wave < 4)
+        state_loop<true, bf16, true>(sm.s, a, o, S);
+      else
+        state_loop<false, bf16, true>(sm.s, a, o, S);
+      if (s_out != nullptr) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) s_out[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] = S[i4];
+      }
     }
     return;
   }
 
-  // items of the queue in chunk order, u = chunk * nch + m (chain qi + n_q m)
-  const int n_q_items = nch * nct, n_items = B * nct * Hv;
+  // item workers: ticket u of the queue -> item (chunk x head); thread 0 decodes it for the workgroup
+  auto item_of = [&](int u) {
+    int m, c;
+    if (ctl.few) {  // chunk order across the chains: u = chunk * nch + m
+      m = u % nch;
+      c = u / nch;
+    } else {  // chain after chain: the last chain m with qpref[m] <= u
+      int lo = 0, hi = nch - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (qpref[mid] <= u) lo = mid;
+        else hi = mid - 1;
+      }
+      m = lo;
+      c = u - qpref[m];
+    }
+    const int ch = qi + ctl.n_q * m;
+    return (chunk0(ch / Hv) + c) * Hv + ch % Hv;
+  };
   for (;;) {
     __syncthreads();  // every thread has read tk (and the LDS of the last item is free)
-    if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 64 * qi + 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+      const int u = __hip_atomic_fetch_add(ctl.tickets + 96 * qi + 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tk = u < n_q_items ? item_of(u) : -1;
+    }
     __syncthreads();
-    const int u = tk;
-    if (u >= n_q_items) break;
-    const int ch = qi + ctl.n_q * (u % nch), c = u / nch;
-    const int b = ch / Hv, h = ch % Hv;
-    const int item = (b * nct + c) * Hv + h;
-    prep_item<TG, GATE>(sm.p, item, q, k, v, g, beta, A_log, dt_bias, nullptr, nullptr, B, n_items, T, Hk, Hv,
+    const int item = tk;
+    if (item < 0) break;
+    if (item >= n_items) continue;  // a chunk past a short chunk table: no workspace (the state job stops before)
+    prep_item<TG, GATE>(sm.p, item, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, n_items, T, Hk, Hv,
                         scale, qk_l2norm, rs, ws);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
     __syncthreads();
@@ -1383,36 +1465,33 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
     p += (size_t)B * (plan.G - 1) * Hv * hs * 4;
     s_start = reinterpret_cast<uint16_t*>(p);
   }
-  // phases 1 and 2 in one overlapped launch: unpacked batches of 8 .. 32 chains on the plain pass
+  // phases 1 and 2 in one overlapped launch: unpacked batches of 8 .. 32 chains (few-chains order) on the plain
+  // pass, packed batches of up to 256 sequences and unpacked batches of more chains (many-chains order)
   const int n_q = std::min(FQ_MAX, std::max(1, device_cus() / 32));  // XCDs (32 CUs each on gfx950)
-  const long n_chains = (long)B * Hv;
-  if (cu_seqlens == nullptr && !segmented && n_chunks > 0 && n_chains >= n_q && n_chains <= (long)FQ_MAX_CHAINS * n_q &&
-      overlap_enabled()) {
+  const long n_chains = (long)N * Hv;
+  const bool few = cu_seqlens == nullptr && n_chains <= (long)FQ_FEW_CHAINS * n_q;
+  const bool fits = few || ((cu_seqlens == nullptr || N <= FQ_MAX_SEQS) &&
+                            (n_chains + n_q - 1) / n_q <= FQ_MAX_QCHAINS);
+  if (!segmented && n_chunks > 0 && n_chains >= n_q && fits && overlap_enabled()) {
     const int n_items = n_chunks * Hv;
     int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
-    const FusedCtl ctl{ctl_base, ctl_base + 64 * FQ_MAX, ctl_base + 64 * (FQ_MAX + 1), n_q};
+    const FusedCtl ctl{ctl_base, ctl_base + 96 * FQ_MAX, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0};
     const int n_ctl = (int)(fused_ctl_bytes(n_items) / 4);
     hipLaunchKernelGGL(zero_ints_kernel, dim3((n_ctl + 255) / 256), dim3(256), 0, s, ctl_base, n_ctl);
     const dim3 grid(P1_WGS_PER_CU * device_cus());
+#define ZGDN_FUSED(TGT, GT)                                                                                        \
+  hipLaunchKernelGGL((chunk_fused_kernel<TGT, GT>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,             \
+                     (const uint16_t*)k, (const uint16_t*)v, (const TGT*)g, (const TGT*)beta, A_log, dt_bias,    \
+                     cu_seqlens, chunk_indices, N, n_chunks, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, \
+                     final_state, (bf16*)o, ctl)
     if (gb_dtype == ZGDN_F32) {
-      if (gate)
-        hipLaunchKernelGGL((chunk_fused_kernel<float, true>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
-                           (const uint16_t*)k, (const uint16_t*)v, (const float*)g, (const float*)beta, A_log,
-                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
-      else
-        hipLaunchKernelGGL((chunk_fused_kernel<float, false>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
-                           (const uint16_t*)k, (const uint16_t*)v, (const float*)g, (const float*)beta, A_log,
-                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+      if (gate) ZGDN_FUSED(float, true);
+      else ZGDN_FUSED(float, false);
     } else {
-      if (gate)
-        hipLaunchKernelGGL((chunk_fused_kernel<bf16, true>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
-                           (const uint16_t*)k, (const uint16_t*)v, (const bf16*)g, (const bf16*)beta, A_log,
-                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
-      else
-        hipLaunchKernelGGL((chunk_fused_kernel<bf16, false>), grid, dim3(P1_THREADS), 0, s, (const uint16_t*)q,
-                           (const uint16_t*)k, (const uint16_t*)v, (const bf16*)g, (const bf16*)beta, A_log,
-                           dt_bias, B, T, Hk, Hv, scale, qk_l2norm, rs, ws, initial_state, final_state, (bf16*)o, ctl);
+      if (gate) ZGDN_FUSED(bf16, true);
+      else ZGDN_FUSED(bf16, false);
     }
+#undef ZGDN_FUSED
     return check_launch(fn);
   }
   if (n_chunks > 0) {
