@@ -39,6 +39,7 @@ namespace zgdn {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int CH = 64;    // chunk length
@@ -381,9 +382,9 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
         const uint4 w = *reinterpret_cast<const uint4*>(row + ((cc + 8 * r) & (DK - 1)));
         const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xffff0000u);
-          ss = fmaf(lo, lo, fmaf(hi, hi, ss));
+        for (int i = 0; i < 4; ++i) {  // both squares of a bf16 pair in one instruction (v_dot2c_f32_bf16)
+          const bf16x2 x = __builtin_bit_cast(bf16x2, u[i]);
+          ss = __builtin_amdgcn_fdot2_f32_bf16(x, x, ss, false);
         }
       }
       const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
