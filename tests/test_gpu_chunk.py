@@ -191,10 +191,10 @@ def test_segmented_state_pass(gdn, cuda, B, T, Hk, Hv, with_state):
                                                        (1, 100, 16, 16, False, True),
                                                        (4, 500, 16, 16, True, True)])
 def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_state):
-    """Unpacked batches of 8 .. 32 (sequence, head) chains take the overlapped launch (phase 1 and the state
-    pass in one kernel, linked by per-chunk ready flags on each XCD). It runs the same arithmetic as the two
-    launches, so the results are bit-identical to them (ZGDN_CHUNK_OVERLAP=0), on two calls in a row (the
-    control block is reset per call), and within tolerance of the oracle. Shapes: the prefill workload, two
+    """The overlapped launch (phase 1 and the state pass in one kernel, linked by per-chunk ready flags on each
+    XCD), forced with ZGDN_CHUNK_OVERLAP=1 (by default it is taken only where it measured faster). It runs the
+    same arithmetic as the two launches, so the results are bit-identical to them (ZGDN_CHUNK_OVERLAP=0), on
+    two calls in a row (the control block is reset per call), and within tolerance of the oracle. Shapes: the prefill workload, two
     sequences with grouped heads and a ragged last chunk, the largest (32 chains) and smallest (8) batches of
     the few-chains order, a sequence shorter than two chunks, and 64 chains (the many-chains order)."""
     announce(f"chunk overlapped B={B} T={T} Hk={Hk} Hv={Hv} gate={gate} state={with_state}")
@@ -227,8 +227,8 @@ def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_stat
                                           ([100] * 40, 4, 8)])
 def test_overlapped_launch_packed(gdn, cuda, monkeypatch, lengths, Hk, Hv):
     """Packed sequences (and their empty, one-token and ragged members) in the overlapped launch's many-chains
-    order: bit-identical to the two launches, within tolerance of the oracle, initial states carried and the
-    empty sequence's state passed through."""
+    order (forced): bit-identical to the two launches, within tolerance of the oracle, initial states carried
+    and the empty sequence's state passed through."""
     announce(f"chunk overlapped packed n={len(lengths)} Hk={Hk} Hv={Hv}")
     cu, chunks = O.chunk_tables(lengths)
     d = O.make_inputs(1, sum(lengths), Hk, Hv, 128, 128, seed=2700 + len(lengths), dtype=torch.bfloat16,

@@ -1359,11 +1359,20 @@ size_t seg_bytes(int B, int T, int Hv, const SegPlan& p) {
   return (size_t)B * T * Hv * DK * 2 + (size_t)B * Hv * hs * (4 * p.G + 4 * (p.G - 1) + 2 * (p.G - 1));
 }
 
-// The overlapped launch is taken unless the environment sets ZGDN_CHUNK_OVERLAP=0 (read at each call): the
-// two-launch form stays reachable for comparison.
-bool overlap_enabled() {
+// Whether an eligible batch takes the overlapped launch. ZGDN_CHUNK_OVERLAP in the environment (read at each
+// call) forces it off ("0") or on ("1"); otherwise it is taken where it measured faster than the two launches
+// on MI355X (same-process comparisons, bf16, dk = dv = 128): few chains only with long sequences (64 chunks:
+// 82.6 against 84.6 us; at 8 .. 32 chunks it was 15-45 % slower), many chains when there are at least 3072
+// chunk x head items and 8 chunks or more per chain on average (+3-11 %: 512 chains of 8 chunks, 256 of 12 or
+// 16, 128 of 32, the 32-sequence packed workload); 256 chains of 8, 128 of 16, 64 of 32 lost 2-15 % (the state
+// pass starts only after the first items, shares its CUs with phase 1, and with a fixed share of state
+// workgroups short or few chains leave them waiting).
+bool overlap_wanted(bool few, long n_items, double chunks_per_chain) {
   const char* e = std::getenv("ZGDN_CHUNK_OVERLAP");
-  return !(e != nullptr && e[0] == '0');
+  if (e != nullptr && e[0] == '0') return false;
+  if (e != nullptr && e[0] == '1') return true;
+  if (few) return chunks_per_chain >= 64;
+  return n_items >= 3072 && chunks_per_chain >= 8;
 }
 
 int device_cus() {
@@ -1466,14 +1475,16 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
     p += (size_t)B * (plan.G - 1) * Hv * hs * 4;
     s_start = reinterpret_cast<uint16_t*>(p);
   }
-  // phases 1 and 2 in one overlapped launch: unpacked batches of 8 .. 32 chains (few-chains order) on the plain
-  // pass, packed batches of up to 256 sequences and unpacked batches of more chains (many-chains order)
+  // phases 1 and 2 in one overlapped launch where it pays (overlap_wanted): unpacked batches of 8 .. 32 chains
+  // (few-chains order) on the plain pass, packed batches of up to 256 sequences and unpacked batches of more
+  // chains (many-chains order)
   const int n_q = std::min(FQ_MAX, std::max(1, device_cus() / 32));  // XCDs (32 CUs each on gfx950)
   const long n_chains = (long)N * Hv;
   const bool few = cu_seqlens == nullptr && n_chains <= (long)FQ_FEW_CHAINS * n_q;
   const bool fits = few || ((cu_seqlens == nullptr || N <= FQ_MAX_SEQS) &&
                             (n_chains + n_q - 1) / n_q <= FQ_MAX_QCHAINS);
-  if (!segmented && n_chunks > 0 && n_chains >= n_q && fits && overlap_enabled()) {
+  if (!segmented && n_chunks > 0 && n_chains >= n_q && fits &&
+      overlap_wanted(few, (long)n_chunks * Hv, (double)n_chunks / std::max(1, N))) {
     const int n_items = n_chunks * Hv;
     int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
     const FusedCtl ctl{ctl_base, ctl_base + 96 * FQ_MAX, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0};
