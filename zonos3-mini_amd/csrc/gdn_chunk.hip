@@ -255,6 +255,22 @@ struct Prep {
   float Fk[CH];  // exp(G_L - G) rk
 };
 
+// Transposed store of one row's 8 columns into a swizzled [.][64] bf16 matrix, together with the lane holding
+// the same columns of the neighbouring row (lane ^ 16, row r ^ 1): the even row's lane stores columns
+// c8 .. c8+3 and the odd row's lane columns c8+4 .. c8+7, each as (even, odd) pairs dst(c, r & ~1 .. +1).
+__device__ __forceinline__ void store_rows_t(uint16_t* dst, int c8, int r, uint4 x) {
+  const bool odd = (r & 1) != 0;
+  const uint32_t s0 = odd ? x.x : x.z, s1 = odd ? x.y : x.w;  // the half the partner stores
+  const uint32_t p0 = __shfl_xor(s0, 16), p1 = __shfl_xor(s1, 16);
+  // (even row words, odd row words) of the 4 columns this lane stores
+  const uint32_t e0 = odd ? p0 : x.x, e1 = odd ? p1 : x.y, o0 = odd ? x.z : p0, o1 = odd ? x.w : p1;
+  const int c = c8 + (odd ? 4 : 0), rp = r & ~1;
+  *reinterpret_cast<uint32_t*>(dst + at16<8>(c, rp)) = (e0 & 0xffffu) | (o0 << 16);
+  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 1, rp)) = (e0 >> 16) | (o0 & 0xffff0000u);
+  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 2, rp)) = (e1 & 0xffffu) | (o1 << 16);
+  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 3, rp)) = (e1 >> 16) | (o1 & 0xffff0000u);
+}
+
 // Row-pair transposed store into a swizzled [.][64] bf16 matrix: dst(c8 + i, r .. r + 1) <- (a[i], b[i]).
 __device__ __forceinline__ void store_pair_t(uint16_t* dst, int c8, int r, uint4 a, uint4 b) {
   const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
@@ -314,8 +330,10 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
     int tz = 0;
     asm volatile("" : "+v"(tz));
     const int tid = (int)threadIdx.x + tz, l = tid & 63;
-    const int p = tid % (CH / 2), c8 = (tid / (CH / 2)) * 8;  // step 1: 32 row pairs x 16 column groups
-    const int r0 = 2 * p, r1 = 2 * p + 1;
+    // step 1: 16 lanes read one whole 256-byte row (8 full cache lines per load instruction); thread (rr, cg)
+    // holds columns c8 .. c8+7 of rows rr and rr + 32
+    const int rr = tid >> 4, c8 = (tid & 15) * 8;
+    const int r0 = rr, r1 = rr + CH / 2;
     const SwLane sw(l);
     const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
     const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
@@ -353,8 +371,12 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r1, c8)]) = q1;
       *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r0, c8)]) = k0;
       *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r1, c8)]) = k1;
-      store_pair_t(sm.KsT, c8, r0, k0, k1);
-      store_pair_t(sm.VsT, c8, r0, v0, v1);
+      // K^T and V^T: rows rr and rr ^ 1 sit in lanes l and l ^ 16, which trade half their columns so that
+      // each stores 4 column pairs of the row pair as 4-byte words
+      store_rows_t(sm.KsT, c8, rr, k0);
+      store_rows_t(sm.KsT, c8, rr + CH / 2, k1);
+      store_rows_t(sm.VsT, c8, rr, v0);
+      store_rows_t(sm.VsT, c8, rr + CH / 2, v1);
     }
     if (wave == P1_WAVES - 1) {
       if (l < cr.len) {
