@@ -398,18 +398,21 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
     if (tid < 2 * CH) {
       const int r = tid & (CH - 1);
       const uint16_t* row = (tid < CH ? sm.u.a.Qs : sm.u.a.Ks) + r * DK;
-      float ss = 0.f;
+      float rf = 1.f;
+      if (qk_l2norm) {
+        float ss = 0.f;
 #pragma unroll
-      for (int cc = 0; cc < DK; cc += 8) {  // chunk (cc / 8 + r) % 16: the rows' reads spread over the banks
-        const uint4 w = *reinterpret_cast<const uint4*>(row + ((cc + 8 * r) & (DK - 1)));
-        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        for (int cc = 0; cc < DK; cc += 8) {  // chunk (cc / 8 + r) % 16: the rows' reads spread over the banks
+          const uint4 w = *reinterpret_cast<const uint4*>(row + ((cc + 8 * r) & (DK - 1)));
+          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // both squares of a bf16 pair in one instruction (v_dot2c_f32_bf16)
-          const bf16x2 x = __builtin_bit_cast(bf16x2, u[i]);
-          ss = __builtin_amdgcn_fdot2_f32_bf16(x, x, ss, false);
+          for (int i = 0; i < 4; ++i) {  // both squares of a bf16 pair in one instruction (v_dot2c_f32_bf16)
+            const bf16x2 x = __builtin_bit_cast(bf16x2, u[i]);
+            ss = __builtin_amdgcn_fdot2_f32_bf16(x, x, ss, false);
+          }
         }
+        rf = rsqrtf(ss + 1e-6f);
       }
-      const float rf = qk_l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
       const float gr = sm.Gs[r];
       if (tid < CH) {
         sm.Pi[r] = scale * rf;
