@@ -981,9 +981,10 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 //
 // One launch in which phase 1 and the state pass run side by side. The state pass of a (sequence, head) chain
 // starts once phase 1 has stored the chain's first chunk and then trails it, instead of waiting for every item
-// of every chain: for few chains (unpacked batches of 8 .. 32 at 8 XCDs) most of phase 1 hides under the
-// state pass, which holds one CU per 16 value rows of each chain; for many chains (packed batches) each
-// chunk's workspace is read back while it is still in the L2 or the last-level cache rather than from HBM.
+// of every chain: for few chains (unpacked batches of 8 .. 32 at 8 XCDs) part of phase 1 hides under the
+// state pass, which holds one CU per 16 value rows of each chain; for many chains (packed batches) the state
+// jobs of early chains run while phase 1 works on later ones. (The bytes moved stay the same: the workspace
+// still goes to memory and back.) Where this pays is measured, see overlap_wanted.
 //
 // Producer and consumers of a chunk's workspace must share one L2: the XCDs' L2 caches are not coherent with
 // each other, and the fences that would make them so write back or drop a whole L2. So every chain belongs to
