@@ -67,6 +67,8 @@ constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
 //   Ob  [vb][tb][l] 4 bf16: Ob[16 tb + 4 (l/16) + i][16 vb + l%16]      (D tiles)
 //   G_L, then padding to a 256-byte multiple.
 // kappa(kk, l, i) = 32 kk + 4 (l/16) + i for i < 4 and 32 kk + 16 + 4 (l/16) + i - 4 for i >= 4.
+// (Phase 1 keeps the k and v rows row-major in LDS and reads the K^T / V^T operands with transposing LDS
+// reads.)
 constexpr size_t WS_WP = 0;
 constexpr size_t WS_QP = WS_WP + CH * DK * 2;
 constexpr size_t WS_KT = WS_QP + CH * DK * 2;
@@ -194,6 +196,44 @@ __device__ __forceinline__ f32x4 stile(const uint16_t* A, int r0, const uint16_t
   return acc;
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes, lane s supplies the address of 4
+// consecutive bf16 (row k0 + s/4, columns c0 + 4 (s%4) .. +3 of a row-major matrix) and lane i receives column
+// c0 + i of rows k0 .. k0 + 3.
+typedef short short4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ short4_t lds_read_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
+}
+
+// MFMA A / B fragment of M^T (rows r0 + lane%16 of M^T = columns of M, k = 32 kk + 8 (lane/16) .. +7 = rows of
+// M) from the row-major swizzled [64][128] bf16 matrix M: two transposing reads of 4 rows each.
+__device__ __forceinline__ bf16x8 tfrag(const uint16_t* M, int r0, int kk) {
+  const int l = lane_id(), s = l & 15;
+  const int k0 = 32 * kk + 8 * (l >> 4) + (s >> 2), c = r0 + 4 * (s & 3);
+  const short4_t lo = lds_read_tr(M + at16<16>(k0, c)), hi = lds_read_tr(M + at16<16>(k0 + 4, c));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// Tile (r0.., c0..) of A . B with A = M^T read transposed from the row-major M (keys x tokens, contraction over
+// tokens [0, kend)) and B given by the swizzled 128-byte-row Bt.
+__device__ __forceinline__ f32x4 stile_ta(const uint16_t* M, int r0, const uint16_t* Bt, int c0, int kend,
+                                          const SwLane& sw, f32x4 acc) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+    if (32 * kk < kend) acc = mfma(tfrag(M, r0, kk), sfrag<8>(Bt, c0, kk, sw), acc);
+  return acc;
+}
+
+// Tile (r0.., c0..) of A . B with A the swizzled 128-byte-row matrix and B = M read transposed from the
+// row-major M (tokens x values, contraction over tokens [0, kend)).
+__device__ __forceinline__ f32x4 stile_tb(const uint16_t* A, int r0, const uint16_t* M, int c0, int kend,
+                                          const SwLane& sw, f32x4 acc) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+    if (32 * kk < kend) acc = mfma(sfrag<8>(A, r0, kk, sw), tfrag(M, c0, kk), acc);
+  return acc;
+}
+
 // 16x16x16 fp32 block product acc += A[ra.., ca..] . B[rb.., cb..] of swizzled 64x64 fp32 matrices.
 __device__ __forceinline__ f32x4 mm16_f32(const float* A, int ra, int ca, const float* B, int rb, int cb, int l,
                                           f32x4 acc) {
@@ -224,11 +264,10 @@ __device__ __forceinline__ void put16_f32(float* M, int r0, int c0, int l, f32x4
 }
 
 struct Prep {
-  // one 32 KiB region reused by phase: raw q, k rows -> A, T (fp32) -> the bf16 forms of T and R -> Ub^T
+  // one 32 KiB region reused by phase: raw q rows -> A, T (fp32) -> the bf16 forms of T and R -> Ub^T
   union {
     struct {
-      uint16_t Qs[CH * DK];  // raw q, k rows, 256-byte rows (operands of K K^T, Q K^T)
-      uint16_t Ks[CH * DK];
+      uint16_t Qs[CH * DK];  // raw q rows, 256-byte rows (A operand of Q K^T)
     } a;
     struct {
       float As[CH * CH];  // strictly lower A (fp32, 256-byte rows), then N_ij = T_ii A_ij in its blocks
@@ -242,8 +281,9 @@ struct Prep {
     } c;
     uint16_t UbT[DV * CH];  // Ub^T (B operand of Ob = P Ub), over TBF and TBT once W' and R are formed
   } u;
-  uint16_t KsT[DK * CH];  // raw k^T: A operand of W'^T, Q'^T; source of the K^T fragments
-  uint16_t VsT[DV * CH];  // v^T: B operand of Ub, and the exact diagonal term
+  uint16_t Ks[CH * DK];  // raw k rows: both operands of K K^T, the B operand of Q K^T; read transposed as the A
+                         // operand of W'^T and Q'^T and for the K^T fragments
+  uint16_t Vs[CH * DV];  // v rows, read transposed as the B operand of Ub and for the exact diagonal term
   uint16_t Ps[CH * CH];   // P (bf16, zero above the diagonal blocks)
   float Gs[CH];
   float Bs[CH];
@@ -254,32 +294,6 @@ struct Prep {
   float Fq[CH];  // s exp(G) rq
   float Fk[CH];  // exp(G_L - G) rk
 };
-
-// Transposed store of one row's 8 columns into a swizzled [.][64] bf16 matrix, together with the lane holding
-// the same columns of the neighbouring row (lane ^ 16, row r ^ 1): the even row's lane stores columns
-// c8 .. c8+3 and the odd row's lane columns c8+4 .. c8+7, each as (even, odd) pairs dst(c, r & ~1 .. +1).
-__device__ __forceinline__ void store_rows_t(uint16_t* dst, int c8, int r, uint4 x) {
-  const bool odd = (r & 1) != 0;
-  const uint32_t s0 = odd ? x.x : x.z, s1 = odd ? x.y : x.w;  // the half the partner stores
-  const uint32_t p0 = __shfl_xor(s0, 16), p1 = __shfl_xor(s1, 16);
-  // (even row words, odd row words) of the 4 columns this lane stores
-  const uint32_t e0 = odd ? p0 : x.x, e1 = odd ? p1 : x.y, o0 = odd ? x.z : p0, o1 = odd ? x.w : p1;
-  const int c = c8 + (odd ? 4 : 0), rp = r & ~1;
-  *reinterpret_cast<uint32_t*>(dst + at16<8>(c, rp)) = (e0 & 0xffffu) | (o0 << 16);
-  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 1, rp)) = (e0 >> 16) | (o0 & 0xffff0000u);
-  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 2, rp)) = (e1 & 0xffffu) | (o1 << 16);
-  *reinterpret_cast<uint32_t*>(dst + at16<8>(c + 3, rp)) = (e1 >> 16) | (o1 & 0xffff0000u);
-}
-
-// Row-pair transposed store into a swizzled [.][64] bf16 matrix: dst(c8 + i, r .. r + 1) <- (a[i], b[i]).
-__device__ __forceinline__ void store_pair_t(uint16_t* dst, int c8, int r, uint4 a, uint4 b) {
-  const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint32_t*>(dst + at16<8>(c8 + 2 * i, r)) = (wa[i] & 0xffffu) | (wb[i] << 16);
-    *reinterpret_cast<uint32_t*>(dst + at16<8>(c8 + 2 * i + 1, r)) = (wa[i] >> 16) | (wb[i] & 0xffff0000u);
-  }
-}
 
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -351,7 +365,7 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       }
     }
 
-    // 1. rows of q, k, v -> LDS (zeros past the chunk end): Q, K row-major, K^T and V^T; gate and G.
+    // 1. rows of q, k, v -> LDS (zeros past the chunk end), row-major; gate and G.
     {
       const uint4 z = make_uint4(0, 0, 0, 0);
       uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
@@ -369,14 +383,10 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       }
       *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r0, c8)]) = q0;
       *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r1, c8)]) = q1;
-      *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r0, c8)]) = k0;
-      *reinterpret_cast<uint4*>(&sm.u.a.Ks[at16<16>(r1, c8)]) = k1;
-      // K^T and V^T: rows rr and rr ^ 1 sit in lanes l and l ^ 16, which trade half their columns so that
-      // each stores 4 column pairs of the row pair as 4-byte words
-      store_rows_t(sm.KsT, c8, rr, k0);
-      store_rows_t(sm.KsT, c8, rr + CH / 2, k1);
-      store_rows_t(sm.VsT, c8, rr, v0);
-      store_rows_t(sm.VsT, c8, rr + CH / 2, v1);
+      *reinterpret_cast<uint4*>(&sm.Ks[at16<16>(r0, c8)]) = k0;
+      *reinterpret_cast<uint4*>(&sm.Ks[at16<16>(r1, c8)]) = k1;
+      *reinterpret_cast<uint4*>(&sm.Vs[at16<16>(r0, c8)]) = v0;
+      *reinterpret_cast<uint4*>(&sm.Vs[at16<16>(r1, c8)]) = v1;
     }
     if (wave == P1_WAVES - 1) {
       if (l < cr.len) {
@@ -397,7 +407,7 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
     // squares runs over the stored chunks in any order
     if (tid < 2 * CH) {
       const int r = tid & (CH - 1);
-      const uint16_t* row = (tid < CH ? sm.u.a.Qs : sm.u.a.Ks) + r * DK;
+      const uint16_t* row = (tid < CH ? sm.u.a.Qs : sm.Ks) + r * DK;
       float rf = 1.f;
       if (qk_l2norm) {
         float ss = 0.f;
@@ -435,7 +445,7 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       if (job < 20) {
         int rb, cb;
         lower_tile(job % 10, rb, cb);
-        acc[m] = stile<16, 16>(job < 10 ? sm.u.a.Ks : sm.u.a.Qs, rb * 16, sm.u.a.Ks, cb * 16, DK, sw, zero4());
+        acc[m] = stile<16, 16>(job < 10 ? sm.Ks : sm.u.a.Qs, rb * 16, sm.Ks, cb * 16, DK, sw, zero4());
       }
     }
     __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
@@ -584,8 +594,8 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
 #pragma unroll
       for (int m = 0; m < 2; ++m) {  // (token tile, k-step): W'^T = K^T TBF^T
         const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        const f32x4 d0 = stile<8, 8>(sm.KsT, 32 * kq, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
-        const f32x4 d1 = stile<8, 8>(sm.KsT, 32 * kq + 16, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
+        const f32x4 d0 = stile_ta(sm.Ks, 32 * kq, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
+        const f32x4 d1 = stile_ta(sm.Ks, 32 * kq + 16, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
         gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
       }
       for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
@@ -601,7 +611,8 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       for (int m = 0; m < DK * CH / 8 / P1_THREADS; ++m) {  // fragment f = 2 w + kk, lane ll
         const int e = tid + P1_THREADS * m;
         const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
-        gKT[e] = *reinterpret_cast<const uint4*>(&sm.KsT[at16<8>(16 * w + (ll & 15), 32 * kk + 8 * (ll >> 4))]);
+        gKT[e] = __builtin_bit_cast(uint4, tfrag(sm.Ks, 16 * w, kk));
+        (void)ll;
       }
     }
     __syncthreads();  // Ub^T overwrites TBF, TBT
@@ -612,9 +623,11 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
 #pragma unroll
       for (int m = 0; m < 4; ++m) {  // (token tile, value block)
         const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
-        const f32x4 u = stile<8, 8>(sm.u.c.LB, 16 * tb, sm.VsT, 16 * vb, tri_kend(tb), sw, zero4());
+        const f32x4 u = stile_tb(sm.u.c.LB, 16 * tb, sm.Vs, 16 * vb, tri_kend(tb), sw, zero4());
         const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
-        const uint2 vv = *reinterpret_cast<const uint2*>(&sm.VsT[at16<8>(n, i0)]);
+        // v[i0 .. i0+3][n] by one transposing read (lane s: row i0 + s/4, columns 16 vb + 4 (s%4) ..)
+        const uint2 vv = __builtin_bit_cast(
+            uint2, lds_read_tr(sm.Vs + at16<16>(i0 + ((l & 15) >> 2), vb * 16 + 4 * (l & 3))));
         const float4 bs = *reinterpret_cast<const float4*>(&sm.Bs[i0]);
         const float4 fk = *reinterpret_cast<const float4*>(&sm.Fk[i0]);
         float ub[4];
@@ -634,8 +647,8 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
 #pragma unroll
       for (int m = 0; m < 2; ++m) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
         const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        f32x4 d0 = stile<8, 8>(sm.KsT, 32 * kq, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
-        f32x4 d1 = stile<8, 8>(sm.KsT, 32 * kq + 16, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
+        f32x4 d0 = stile_ta(sm.Ks, 32 * kq, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
+        f32x4 d1 = stile_ta(sm.Ks, 32 * kq + 16, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
         const float fq = sm.Fq[16 * tb + (l & 15)];
         const uint2 c0 = cq[m][0], c1 = cq[m][1];
         d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
@@ -657,7 +670,7 @@ __device__ __forceinline__ void prep_item(Prep& sm, int item,
       }
       if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
     }
-    __syncthreads();  // the next item's rows overwrite Qs / Ks (aliasing Rs / Ub^T) and K^T, V^T
+    __syncthreads();  // the next item's rows overwrite Qs (aliasing Rs / Ub^T), Ks and Vs
   }
 }
 
