@@ -250,3 +250,77 @@ def test_overlapped_launch_packed(gdn, cuda, monkeypatch, lengths, Hk, Hv):
     for i, n in enumerate(lengths):
         if n == 0:
             assert torch.equal(s1[i].cpu(), d["s0"][i])
+
+
+def _random_case(rng: "torch.Generator"):
+    """One seeded batch: 1-9 packed sequences whose lengths mix the chunk edges (0, 1, 63, 64, 65, 128) with
+    uniform draws up to 900 tokens, 1-8 key heads with 1 or 2 value heads each, and random switches for the
+    initial states, the in-kernel gate, bf16 gate inputs, beta given as logits and the in-kernel L2 norm."""
+    def pick(n):
+        return int(torch.randint(0, n, (1,), generator=rng))
+    edges = [0, 1, 63, 64, 65, 128]
+    n = 1 + pick(9)
+    lengths = [edges[pick(len(edges))] if pick(2) else 1 + pick(900) for _ in range(n)]
+    if sum(lengths) == 0:
+        lengths[0] = 1 + pick(200)
+    hk = [1, 2, 4, 8][pick(4)]
+    return dict(lengths=lengths, Hk=hk, Hv=hk * (1 + pick(2)), state=bool(pick(2)), gate=bool(pick(2)),
+                bf16_gates=bool(pick(2)), beta_logit=bool(pick(2)), l2=bool(pick(2)))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_packed_batches(gdn, cuda, monkeypatch, case):
+    """Seeded random packed batches through the library's own choice of launch form, against the oracle, and
+    bit-identical to the overlapped launch (ZGDN_CHUNK_OVERLAP=1) and the two-launch form (=0). The inputs are drawn
+    as for the configurations, except that with the in-kernel L2 norm q and k are raw N(0,1) rows, g is
+    the raw gate input when the gate is in the kernel, and beta is its logit when so flagged; the oracle
+    takes the rows normalised, the log decay and sigmoid(beta) formed from the same inputs in float32."""
+    rng = torch.Generator().manual_seed(3100 + case)
+    c = _random_case(rng)
+    lengths, Hk, Hv = c["lengths"], c["Hk"], c["Hv"]
+    announce(f"chunk random case={case} {c}")
+    cu, chunks = O.chunk_tables(lengths)
+    T, N = sum(lengths), len(lengths)
+    d = O.make_inputs(1, T, Hk, Hv, 128, 128, seed=3200 + case, dtype=torch.bfloat16, state_std=0.02, n_states=N)
+    q_ref, k_ref = d["q"].float(), d["k"].float()
+    if c["l2"]:  # raw rows in, normalised in the kernel; the oracle normalises the same bf16 rows
+        d["q"] = torch.randn(1, T, Hk, 128, generator=rng).to(torch.bfloat16)
+        d["k"] = torch.randn(1, T, Hk, 128, generator=rng).to(torch.bfloat16)
+        q_ref, k_ref = O.l2norm(d["q"]), O.l2norm(d["k"])
+    g_log, beta_ref = d["g"].float(), d["beta"].float()
+    gdt = torch.bfloat16 if c["bf16_gates"] else torch.float32
+    kw = {}
+    g_in, beta_in = d["g"].to(gdt), d["beta"].to(gdt)
+    if c["gate"]:
+        a = torch.randn(1, T, Hv, generator=rng).to(gdt)
+        A_log, dt_bias = 0.3 * torch.randn(Hv, generator=rng), 0.3 * torch.randn(Hv, generator=rng)
+        kw.update(A_log=A_log.to(cuda), dt_bias=dt_bias.to(cuda))
+        g_in = a
+        g_log = -A_log.exp() * F.softplus(a.float() + dt_bias)
+    elif c["bf16_gates"]:
+        g_log = g_in.float()
+    if c["beta_logit"]:
+        b = torch.randn(1, T, Hv, generator=rng).to(gdt)
+        beta_in, beta_ref = b, torch.sigmoid(b.float())
+        kw["beta_is_logit"] = True
+    elif c["bf16_gates"]:
+        beta_ref = beta_in.float()
+    s0 = d["s0"].to(cuda) if c["state"] else None
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=cuda)
+    ch_t = torch.tensor(chunks, dtype=torch.int32, device=cuda)
+    args = (d["q"].to(cuda), d["k"].to(cuda), d["v"].to(cuda), g_in.to(cuda), beta_in.to(cuda))
+    runs = []
+    for overlap in (None, "1", "0"):
+        if overlap is None:
+            monkeypatch.delenv("ZGDN_CHUNK_OVERLAP", raising=False)
+        else:
+            monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
+        runs.append(gdn.chunk_fwd(*args, initial_state=s0, cu_seqlens=cu_t, chunk_indices=ch_t,
+                                  use_qk_l2norm=c["l2"], **kw))
+    torch.cuda.synchronize()
+    (o1, s1), (o2, s2), (o0, s0_) = runs
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    assert torch.equal(o1, o0) and torch.equal(s1, s0_)
+    o_ref, s_ref = O.gated_delta_recurrence(q_ref, k_ref, d["v"].float(), g_log, beta_ref, None,
+                                            d["s0"] if c["state"] else None, cu_seqlens=cu)
+    _check(o1.cpu(), s1.cpu(), o_ref, s_ref)
