@@ -4,8 +4,9 @@
 
 Headline workload (``value``): the single-token recurrent decode step over B=64 independent streams,
 H=16 heads, dk=dv=128, bf16 q/k/v/o, fp32 state ~N(0, 0.02) updated in place; one step = one launch over
-the whole batch; 8 consecutive steps are captured in one HIP graph and replayed.
-``value`` = 64 tokens x K steps / wall time of the K steps.
+the whole batch. Exactly K consecutive steps are captured in one HIP graph; after W untimed warm-up steps
+the graph is replayed in 7 timed windows (each bracketed by a device synchronisation on both sides) and
+``value`` = 64 tokens x K steps / the median window's wall time.
 
 ``roofline``: algorithmic bytes of one decode launch (132,104 B per token-head: fp32 state read + write,
 bf16 q, k, v, o, fp32 g and beta; x 1024 token-heads = 135,274,496 B) / its mean duration, measured with
@@ -16,7 +17,7 @@ MFMA roofline: 2 C^2 (3 dk + 2 dv) + 6 C dk dv + C^3/3 flops per chunk and head 
 mean duration of the path's kernels, against the 2.5 PFLOP/s dense bf16 peak.
 
 ``cpu_baseline``: the CPU oracle (a restatement of the reference's torch token loop) on the host cores, on
-the same decode step (median of 5 runs after one warm-up).
+the same decode step (median of 5 runs after one warm-up), with all cores and with one thread.
 """
 
 from __future__ import annotations
@@ -66,7 +67,7 @@ def _decode_inputs(torch, dev):
     return d, {n: d[n][:, 0].to(dev) for n in ("q", "k", "v", "g", "beta")}, d["s0"].to(dev)
 
 
-STEPS_PER_GRAPH = 8
+WINDOWS = 7  # timed replays of the K-step graph; the headline is their median
 
 
 def kernel_ms(torch, stream, fn, n):
@@ -95,30 +96,32 @@ def bench_decode(torch, gdn, steps, warmup):
     def step():
         gdn.decode_step(x["q"], x["k"], x["v"], x["g"], x["beta"], state)
 
+    steps = max(1, steps)
     with torch.cuda.stream(stream):
         for _ in range(3):
             step()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()  # STEPS_PER_GRAPH consecutive steps, state carried in place
+        graph = torch.cuda.CUDAGraph()  # exactly `steps` consecutive steps, the state carried in place
         with torch.cuda.graph(graph, stream=stream):
-            for _ in range(STEPS_PER_GRAPH):
+            for _ in range(steps):
                 step()
-        replays = max(1, -(-steps // STEPS_PER_GRAPH))
-        for _ in range(max(1, warmup // STEPS_PER_GRAPH)):
+        for _ in range(warmup):  # untimed warm-up steps
+            step()
+        walls = []
+        for _ in range(WINDOWS):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
             graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(replays):
-            graph.replay()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    done = replays * STEPS_PER_GRAPH
+            torch.cuda.synchronize()
+            walls.append(time.perf_counter() - t0)
+    wall = statistics.median(walls)
     k_ms = kernel_ms(torch, stream, step, 200)
     bytes_per_launch = DECODE_BYTES_PER_TOKEN_HEAD * DECODE["B"] * DECODE["H"]
     return {
-        "steps": done,
-        "tokens_per_s": DECODE["B"] * done / wall,
-        "ms_per_step": wall * 1e3 / done,
+        "steps": steps,
+        "tokens_per_s": DECODE["B"] * steps / wall,
+        "ms_per_step": wall * 1e3 / steps,
+        "window_ms": [round(w * 1e3, 4) for w in walls],
         "kernel_ms": k_ms,
         "bytes_per_launch": bytes_per_launch,
         "achieved_gbs": bytes_per_launch / (k_ms * 1e-3) / 1e9,
@@ -145,11 +148,8 @@ def bench_prefill(torch, gdn, reps=50):
 
     ms = kernel_ms(torch, stream, run, reps)
     # the same call through the two separate launches (phase 1, then the state pass), for comparison
-    os.environ["ZGDN_CHUNK_OVERLAP"] = "0"
-    try:
+    with gdn.ops.launch_form(0):
         ms_two = kernel_ms(torch, stream, run, reps)
-    finally:
-        del os.environ["ZGDN_CHUNK_OVERLAP"]
     flops = PREFILL_FLOP_PER_CHUNK_HEAD * (c["T"] // c["C"]) * c["H"] * c["B"]
     tflops = flops / (ms * 1e-3) / 1e12
     return {
@@ -184,11 +184,9 @@ def bench_varlen(torch, gdn, reps=20):
     from oracle import gdn_oracle as O
 
     dev = torch.device("cuda:0")
-    lengths = varlen_lengths(torch)
+    lengths, d = varlen_inputs(torch)
     total = sum(lengths)
     c = VARLEN
-    d = O.make_inputs(1, total, c["H"], c["H"], c["K"], c["V"], seed=1004, dtype=torch.bfloat16, state_std=0.02,
-                      n_states=c["n_seqs"])
     x = {n: d[n].to(dev) for n in ("q", "k", "v", "g", "beta", "s0")}
     cu, chunks = O.chunk_tables(lengths)
     cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
@@ -218,10 +216,10 @@ FUSED_BYTES_PER_STEP = (2 * 256 * 16 * 128 * 128 * 4 + 2 * 256 * 4096 * 3 * 2 + 
                         + 2 * 256 * 16 * 128 * 2 + 2 * 256 * 16 * 2)
 
 
-def bench_fused(torch, gdn, steps_per_graph=16):
-    """Streaming decode of the whole GDN block: B=256 streams x 512 consecutive single-token steps, 8 q/k
-    heads shared by 16 v heads, conv width 4, fp32 state carried across steps, eps 1e-6."""
-    dev = torch.device("cuda:0")
+def fused_inputs(torch, dev):
+    """The streaming-decode workload's seeded inputs on ``dev``: per step x_qkv [S, B, C] (C = 2 Hk K + Hv K),
+    z [S, B, Hv, K], a, b [S, B, Hv] ~ N(0,1) bf16; conv weight [C, 4] ~ N(0, 0.2); norm weight 1 + 0.1 N(0,1);
+    A_log = dt_bias = 0; the conv cache [B, C, 3] and fp32 state [B, Hv, K, K] start at zero."""
     c = FUSED
     B, S, Hk, Hv, K = c["B"], c["steps"], c["Hk"], c["Hv"], c["K"]
     C = 2 * Hk * K + Hv * K
@@ -237,6 +235,27 @@ def bench_fused(torch, gdn, steps_per_graph=16):
     dt_bias = torch.zeros(Hv, device=dev)
     cache = torch.zeros(B, C, 3, device=dev, dtype=bf)
     state = torch.zeros(B, Hv, K, K, device=dev)
+    return xs, zs, as_, bs, w, nw, A_log, dt_bias, cache, state
+
+
+def varlen_inputs(torch):
+    """The packed-prefill workload's seeded CPU inputs: (lengths, oracle-style input dict)."""
+    from oracle import gdn_oracle as O
+
+    c = VARLEN
+    lengths = varlen_lengths(torch)
+    d = O.make_inputs(1, sum(lengths), c["H"], c["H"], c["K"], c["V"], seed=1004, dtype=torch.bfloat16,
+                      state_std=0.02, n_states=c["n_seqs"])
+    return lengths, d
+
+
+def bench_fused(torch, gdn, steps_per_graph=16):
+    """Streaming decode of the whole GDN block: B=256 streams x 512 consecutive single-token steps, 8 q/k
+    heads shared by 16 v heads, conv width 4, fp32 state carried across steps, eps 1e-6."""
+    dev = torch.device("cuda:0")
+    c = FUSED
+    B, S = c["B"], c["steps"]
+    xs, zs, as_, bs, w, nw, A_log, dt_bias, cache, state = fused_inputs(torch, dev)
     stream = torch.cuda.Stream(dev)
 
     def step(t):
@@ -498,40 +517,66 @@ def calibrate_copy(torch):
     torch.cuda.synchronize()
 
 
+def _host_threads() -> int:
+    """Host cores this process may use (the GPU host's CPU share, not the machine's count)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return max(1, os.cpu_count() or 1)
+
+
+def _cpu_median(torch, fn, threads, runs=5):
+    """Median seconds of ``runs`` calls of fn after one warm-up, with ``threads`` torch threads."""
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        fn()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    return statistics.median(times)
+
+
 def cpu_baseline_prefill(torch):
-    """The CPU oracle on the whole prefill workload (B=1, T=4096, H=16, bf16 inputs), one timed run."""
+    """The CPU oracle on the whole prefill workload (B=1, T=4096, H=16, bf16 inputs): median of 5 runs after a
+    warm-up, with all host cores and with one thread."""
     from oracle import gdn_oracle as O
 
-    torch.set_num_threads(os.cpu_count() or 1)
     c = PREFILL
     d = O.make_inputs(c["B"], c["T"], c["H"], c["H"], c["K"], c["V"], seed=1003, dtype=torch.bfloat16)
-    t0 = time.perf_counter()
-    O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
-    sec = time.perf_counter() - t0
-    return {"value": round(c["T"] / sec, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+
+    def run():
+        O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+
+    threads = _host_threads()
+    sec = _cpu_median(torch, run, threads)
+    sec1 = _cpu_median(torch, run, 1)
+    return {"value": round(c["T"] / sec, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "single_thread": {"value": round(c["T"] / sec1, 1), "cores": 1},
             "sample": "the whole prefill workload (T=4096, H=16) through the torch CPU restatement of the "
-                      "reference token loop, one run"}
+                      "reference token loop, median of 5 runs after 1 warm-up"}
 
 
 def cpu_baseline_decode(torch):
+    """The CPU oracle on one decode step of all 64 streams: median of 5 runs after a warm-up, with all host
+    cores and with one thread."""
     from oracle import gdn_oracle as O
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
     d, _, _ = _decode_inputs(torch, torch.device("cpu"))
     args = (d["q"], d["k"], d["v"], d["g"], d["beta"], None, d["s0"])
-    O.gated_delta_recurrence(*args)
-    times = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        O.gated_delta_recurrence(*args)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    threads = _host_threads()
+    med = _cpu_median(torch, lambda: O.gated_delta_recurrence(*args), threads)
+    med1 = _cpu_median(torch, lambda: O.gated_delta_recurrence(*args), 1)
     return {
-        "value": DECODE["B"] / med,
+        "value": round(DECODE["B"] / med, 1),
         "unit": "tokens/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "kind": "port",
+        "single_thread": {"value": round(DECODE["B"] / med1, 1), "cores": 1},
         "sample": "one decode step of all 64 streams (B=64, H=16, d=128), torch CPU restatement of the "
                   "reference token loop, median of 5 runs after 1 warm-up",
     }
@@ -573,6 +618,7 @@ def main():
         "steps": dec["steps"],
         "warmup": a.warmup,
         "ms_per_step": round(dec["ms_per_step"], 5),
+        "window_ms": dec["window_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -580,7 +626,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "recurrent decode step: B=64 streams, H=16, dk=dv=128, bf16 q/k/v/o, fp32 state "
-                        "~N(0,0.02) updated in place; one launch per step, 8 steps per HIP graph replay",
+                        "~N(0,0.02) updated in place; one launch per step; K steps per HIP graph replay, "
+                        f"median of {WINDOWS} timed windows",
             "batch": 64, "heads": 16, "dk": 128, "dv": 128, "parallelism": "single GPU",
         },
         "roofline": {

@@ -60,10 +60,38 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
  * in one launch, side by side, where that measured faster than two launches: one sequence of 16 heads and
  * 4096 tokens and similar (8 .. 32 (sequence, head) chains of 64 chunks or more), and packed or batched
  * sequences with at least 3072 chunk x head items and 8 chunks or more per chain on average (up to 256 packed
- * sequences). The environment variable ZGDN_CHUNK_OVERLAP=0 / =1 turns that off / on for every eligible batch
- * (the same results, bit for bit).
+ * sequences). zgdn_chunk_set_launch_form overrides that choice (the same results, bit for bit).
  */
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
+
+/*
+ * Launch form of zgdn_chunk_fwd for this process: -1 the library's choice (above), 0 always phase 1 and the
+ * state pass as two launches, 1 the overlapped launch for every eligible batch. The initial value is read once,
+ * when the library is loaded, from the environment variable ZGDN_CHUNK_OVERLAP ("0" or "1"; otherwise -1); no
+ * call reads the environment. This build's own control, with no counterpart in the reference (FLA picks its
+ * launches itself). zgdn_chunk_get_launch_form returns the current value.
+ */
+int zgdn_chunk_set_launch_form(int form);
+int zgdn_chunk_get_launch_form(void);
+
+/*
+ * Device status of the chunked path. The overlapped launch's state pass waits for each chunk's phase-1 results
+ * with a bounded spin; a wait that runs out (which a correct launch never reaches) sets ZGDN_STATUS_WAIT_GAVE_UP
+ * in a sticky per-device status word, lets every kernel end, and leaves o and the final states of that call
+ * undefined. zgdn_chunk_status synchronises the current device, stores the word in *status (0 = no error since
+ * it was last cleared) and clears it when `clear` is nonzero. It is not a hot-path call: launches stay
+ * asynchronous and never read the word. (The reference's FLA launches have no such wait.)
+ */
+enum { ZGDN_STATUS_WAIT_GAVE_UP = 1 };
+int zgdn_chunk_status(int* status, int clear);
+
+/*
+ * Test control of the overlapped launch's waits for this process: `spins` bounds each wait (0 = the default,
+ * about a few tenths of a second), and never_ready != 0 makes every wait treat its chunk as not ready, so that
+ * each wait runs out after `spins` tries -- the way tests drive the error path of zgdn_chunk_status while
+ * every kernel still ends normally. No counterpart in the reference.
+ */
+int zgdn_chunk_set_wait_limit(int spins, int never_ready);
 
 /*
  * Extra workspace bytes (after zgdn_chunk_workspace_size's) with which zgdn_chunk_fwd runs an unpacked batch of

@@ -24,7 +24,8 @@ def test_header_declares_entry_points():
     assert {"zgdn_last_error", "zgdn_abi_version", "zgdn_recurrent_fwd", "zgdn_chunk_fwd", "zgdn_chunk_workspace_size",
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
             "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route", "zgdn_accent_workspace_size",
-            "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size"} == _declared()
+            "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size", "zgdn_chunk_set_launch_form",
+            "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -154,3 +155,41 @@ def test_host_validation_refuses_cpu_tensors(gdn):
     q = torch.zeros(1, 2, 1, 128)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         gdn.recurrent_fwd(q, q, q, torch.zeros(1, 2, 1), torch.zeros(1, 2, 1))
+
+
+def test_launch_form_and_wait_limit_controls(gdn):
+    """The process-wide launch-form switch (no environment read per call) and the wait-limit test switch:
+    valid values are taken and restored, invalid ones rejected with a message, without a device."""
+    from importlib import import_module
+
+    native = import_module("zonos3-mini_amd._native")
+    ops = import_module("zonos3-mini_amd.ops")
+    lib = native.lib()
+    before = lib.zgdn_chunk_get_launch_form()
+    with ops.launch_form(0):
+        assert lib.zgdn_chunk_get_launch_form() == 0
+        with ops.launch_form(1):
+            assert lib.zgdn_chunk_get_launch_form() == 1
+        assert lib.zgdn_chunk_get_launch_form() == 0
+    assert lib.zgdn_chunk_get_launch_form() == before
+    assert lib.zgdn_chunk_set_launch_form(2) == native.EINVAL
+    assert b"form 2" in lib.zgdn_last_error()
+    assert lib.zgdn_chunk_set_wait_limit(-1, 0) == native.EINVAL
+    assert lib.zgdn_chunk_set_wait_limit(0, 0) == native.OK
+    assert lib.zgdn_chunk_status(None, 0) == native.EINVAL
+
+
+def test_launch_form_reads_the_environment_once_at_load():
+    """ZGDN_CHUNK_OVERLAP is read when the library is loaded (a fresh process), not at each call."""
+    import os
+    import subprocess
+    import sys
+
+    code = ("import importlib, os; n = importlib.import_module('zonos3-mini_amd._native'); lib = n.lib(); "
+            "a = lib.zgdn_chunk_get_launch_form(); os.environ['ZGDN_CHUNK_OVERLAP'] = '1'; "
+            "print(a, lib.zgdn_chunk_get_launch_form())")
+    env = dict(os.environ, ZGDN_CHUNK_OVERLAP="0")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.split() == ["0", "0"]

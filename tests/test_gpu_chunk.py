@@ -190,10 +190,10 @@ def test_segmented_state_pass(gdn, cuda, B, T, Hk, Hv, with_state):
                                                        (1, 192, 8, 8, True, False),
                                                        (1, 100, 16, 16, False, True),
                                                        (4, 500, 16, 16, True, True)])
-def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_state):
+def test_overlapped_launch(gdn, cuda, B, T, Hk, Hv, gate, with_state):
     """The overlapped launch (phase 1 and the state pass in one kernel, linked by per-chunk ready flags on each
-    XCD), forced with ZGDN_CHUNK_OVERLAP=1 (by default it is taken only where it measured faster). It runs the
-    same arithmetic as the two launches, so the results are bit-identical to them (ZGDN_CHUNK_OVERLAP=0), on
+    XCD), forced with launch form 1 (by default it is taken only where it measured faster). It runs the
+    same arithmetic as the two launches, so the results are bit-identical to them (launch form 0), on
     two calls in a row (the control block is reset per call), and within tolerance of the oracle. Shapes: the prefill workload, two
     sequences with grouped heads and a ragged last chunk, the largest (32 chains) and smallest (8) batches of
     the few-chains order, a sequence shorter than two chunks, and 64 chains (the many-chains order)."""
@@ -210,9 +210,9 @@ def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_stat
         kw = dict(A_log=A_log.to(cuda), dt_bias=dt_bias.to(cuda))
         g_in, g_log = a.to(cuda), -A_log.exp() * F.softplus(a + dt_bias)
     runs = []
-    for overlap in ("1", "1", "0"):
-        monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
-        runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], g_in, x["beta"], initial_state=s0, **kw))
+    for form in (1, 1, 0):
+        with gdn.ops.launch_form(form):
+            runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], g_in, x["beta"], initial_state=s0, **kw))
     torch.cuda.synchronize()
     (o1, s1), (o2, s2), (o0, s0_) = runs
     assert torch.equal(o1, o0) and torch.equal(s1, s0_)
@@ -225,7 +225,7 @@ def test_overlapped_launch(gdn, cuda, monkeypatch, B, T, Hk, Hv, gate, with_stat
 @pytest.mark.parametrize("lengths,Hk,Hv", [([64, 1, 130, 0, 70, 200, 63, 128], 2, 4),
                                           ([700, 64, 1000, 3, 512, 129, 66, 2048, 300, 90, 1, 450], 8, 16),
                                           ([100] * 40, 4, 8)])
-def test_overlapped_launch_packed(gdn, cuda, monkeypatch, lengths, Hk, Hv):
+def test_overlapped_launch_packed(gdn, cuda, lengths, Hk, Hv):
     """Packed sequences (and their empty, one-token and ragged members) in the overlapped launch's many-chains
     order (forced): bit-identical to the two launches, within tolerance of the oracle, initial states carried
     and the empty sequence's state passed through."""
@@ -237,10 +237,10 @@ def test_overlapped_launch_packed(gdn, cuda, monkeypatch, lengths, Hk, Hv):
     cu_t = torch.tensor(cu, dtype=torch.int32, device=cuda)
     ch_t = torch.tensor(chunks, dtype=torch.int32, device=cuda)
     runs = []
-    for overlap in ("1", "1", "0"):
-        monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
-        runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t,
-                                  chunk_indices=ch_t))
+    for form in (1, 1, 0):
+        with gdn.ops.launch_form(form):
+            runs.append(gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"],
+                                      cu_seqlens=cu_t, chunk_indices=ch_t))
     torch.cuda.synchronize()
     (o1, s1), (o2, s2), (o0, s0_) = runs
     assert torch.equal(o1, o0) and torch.equal(s1, s0_)
@@ -269,9 +269,9 @@ def _random_case(rng: "torch.Generator"):
 
 
 @pytest.mark.parametrize("case", range(8))
-def test_random_packed_batches(gdn, cuda, monkeypatch, case):
+def test_random_packed_batches(gdn, cuda, case):
     """Seeded random packed batches through the library's own choice of launch form, against the oracle, and
-    bit-identical to the overlapped launch (ZGDN_CHUNK_OVERLAP=1) and the two-launch form (=0). The inputs are drawn
+    bit-identical to the overlapped launch (launch form 1) and the two-launch form (0). The inputs are drawn
     as for the configurations, except that with the in-kernel L2 norm q and k are raw N(0,1) rows, g is
     the raw gate input when the gate is in the kernel, and beta is its logit when so flagged; the oracle
     takes the rows normalised, the log decay and sigmoid(beta) formed from the same inputs in float32."""
@@ -310,13 +310,10 @@ def test_random_packed_batches(gdn, cuda, monkeypatch, case):
     ch_t = torch.tensor(chunks, dtype=torch.int32, device=cuda)
     args = (d["q"].to(cuda), d["k"].to(cuda), d["v"].to(cuda), g_in.to(cuda), beta_in.to(cuda))
     runs = []
-    for overlap in (None, "1", "0"):
-        if overlap is None:
-            monkeypatch.delenv("ZGDN_CHUNK_OVERLAP", raising=False)
-        else:
-            monkeypatch.setenv("ZGDN_CHUNK_OVERLAP", overlap)
-        runs.append(gdn.chunk_fwd(*args, initial_state=s0, cu_seqlens=cu_t, chunk_indices=ch_t,
-                                  use_qk_l2norm=c["l2"], **kw))
+    for form in (-1, 1, 0):
+        with gdn.ops.launch_form(form):
+            runs.append(gdn.chunk_fwd(*args, initial_state=s0, cu_seqlens=cu_t, chunk_indices=ch_t,
+                                      use_qk_l2norm=c["l2"], **kw))
     torch.cuda.synchronize()
     (o1, s1), (o2, s2), (o0, s0_) = runs
     assert torch.equal(o1, o2) and torch.equal(s1, s2)

@@ -186,3 +186,82 @@ def test_layer_with_weights_read_from_gguf(gdn, cuda, tmp_path):
         y_ref, conv_ref, state_ref, _ = O.gdn_layer(x[lo:hi], read, conv_ref, state_ref, heads=HEADS, head_dim=HD)
         assert rel_err(y.cpu(), y_ref) < 2e-2, (lo, rel_err(y.cpu(), y_ref))
         assert rel_err(cache.gdn_state[0].cpu(), state_ref) < 1e-3, lo
+
+
+def _fork(cache: _Cache, deep: bool) -> _Cache:
+    """LMCache.fork (lm.py:353-359) clones every tensor (deep); a shallow fork shares the tensors, so a drop-in
+    that wrote into the tensors it was handed would show up in the parent."""
+    if deep:
+        return _Cache({k: v.clone() for k, v in cache.gdn_state.items()},
+                      {k: v.clone() for k, v in cache.conv_state.items()})
+    return _Cache(dict(cache.gdn_state), dict(cache.conv_state))
+
+
+@pytest.mark.parametrize("deep", [True, False])
+def test_fork_isolates_caches(gdn, cuda, deep):
+    """model/tests/test_reference_lm.py:139-154 through the drop-in: after a 60-row prefill the cache is forked;
+    the child takes two decode rows (the fused in-place kernel) and a 70-row prefill (the chunked path); the
+    parent's state and conv history stay bit-identical to a snapshot, and the parent's own next decode row
+    equals the child's first bit for bit. With a shallow fork the child shares the parent's tensors, so this
+    also shows that no path writes into the tensors it reads."""
+    announce(f"layer drop-in fork isolation deep={deep}")
+    layer = importlib.import_module("zonos3-mini_amd.layer")
+    w = _weights(4401, torch.bfloat16)
+    model = _Model(w, cuda)
+    layer.patch(model)
+    x = torch.randn(133, DIM, generator=torch.Generator().manual_seed(4402)).to(torch.bfloat16).to(cuda)
+    cache = _Cache()
+    model._gdn(x[:60], 0, cache)
+    snapshot = _fork(cache, deep=True)
+    child = _fork(cache, deep)
+    a = model._gdn(x[60:61], 0, child)
+    model._gdn(x[61:62], 0, child)
+    model._gdn(x[62:132], 0, child)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.gdn_state[0], snapshot.gdn_state[0])
+    assert torch.equal(cache.conv_state[0], snapshot.conv_state[0])
+    assert not torch.equal(child.gdn_state[0], snapshot.gdn_state[0])
+    b = model._gdn(x[60:61], 0, cache)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+class _CapturingModel(_Model):
+    """_Model with lm.py's capture hook: _save stores float32 CPU copies under the given names (lm.py:498-500)."""
+
+    def __init__(self, w, device):
+        super().__init__(w, device)
+        self._capture = {}
+
+    def _save(self, name, tensor):
+        self._capture[name] = tensor.detach().float().cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_capture_names_and_values(gdn, cuda, dtype):
+    """The golden-dump hook (lm.py:588-601; tools/dump_golden.py) through the drop-in: a 40-row prefill then a
+    decode row with capture on save exactly lm.py's ten gdn_*_<layer> names, and every value matches the
+    oracle's captures of the same rows (fp32: 1e-4 relative; bf16: 2e-2 relative, 1e-3 on the fp32 state; the
+    conv output and history compare to the GEMM's rounding, which the GPU and the CPU do differently)."""
+    announce(f"layer drop-in captures {dtype}")
+    layer = importlib.import_module("zonos3-mini_amd.layer")
+    w = _weights(4501, dtype)
+    model = _CapturingModel(w, cuda)
+    layer.patch(model)
+    x = torch.randn(41, DIM, generator=torch.Generator().manual_seed(4502)).to(dtype)
+    cache = _Cache()
+    conv_ref = state_ref = None
+    names = ("gdn_conv", "gdn_q", "gdn_k", "gdn_v", "gdn_decay", "gdn_beta", "gdn_recurrent", "gdn_gated",
+             "gdn_state", "gdn_conv_state")
+    bf16 = dtype == torch.bfloat16
+    for lo, hi in ((0, 40), (40, 41)):
+        model._capture = {}
+        model._gdn(x[lo:hi].to(cuda), 0, cache)
+        torch.cuda.synchronize()
+        _, conv_ref, state_ref, cap = O.gdn_layer(x[lo:hi], w, conv_ref, state_ref, heads=HEADS, head_dim=HD)
+        assert set(model._capture) == {f"{n}_0" for n in names}
+        for n in names:
+            got, want = model._capture[f"{n}_0"], cap[n].float()
+            assert got.shape == want.shape, (n, got.shape, want.shape)
+            tol = (1e-3 if n == "gdn_state" else 2e-2) if bf16 else 1e-4
+            assert rel_err(got, want) < tol, (lo, n, rel_err(got, want))

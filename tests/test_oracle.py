@@ -379,3 +379,112 @@ def test_accent_shift_pins():
     assert np.abs(both - O.accent_shift_np(x, down, up, ma.numpy()) - O.accent_shift_np(x, down, up, mb.numpy())).max() < 1e-9
     # the torch restatement (fp32) agrees with the float64 statement
     assert rel_err(O.accent_shift(x, down, up, ma + mb, y), O.accent_shift_np(x, down, up, ma + mb, y)) < 1e-5
+
+
+# ---------------------------------------------------------------------- whole layer: a known answer (lm.py:556)
+
+
+def _kat_layer():
+    """A layer whose answer is fixed by hand: 2 heads of 4, in_proj = identity (the input row is the projection
+    q|k|v | z | a | b in lm.py:562's order), conv taking only the current input (newest tap 1), A_log =
+    dt_bias = 0, wo = identity. Three tokens:
+      1. a = -30, b = +30 (decay 1, beta 1), q = k = 3 e_h (unit after SiLU and L2), small v: from the zero
+         state o_h = beta (k.q) scale silu(v_h), small enough that the norm's eps (1e-5) matters;
+      2. the same k, a new v, beta 1: the delta rule overwrites, S_h = silu(v2_h) k_h^T; head 0 reads along
+         k (o = S k scale), head 1 reads along an orthogonal q (o = 0);
+      3. a = 0 (decay exp(-softplus(0)) = 1/2), b = -30 (beta 0): S halves, q = k.
+    Returns (x, weights, expected y, expected final state, expected conv history (the three raw inputs))."""
+    heads, hd = 2, 4
+    inner = heads * hd
+    e = torch.eye(hd, dtype=torch.float64)
+    s3 = 3.0 * torch.sigmoid(torch.tensor(3.0, dtype=torch.float64))  # silu(3)
+    c = s3 / torch.sqrt(s3 * s3 + 1e-6)  # |l2norm(silu(3) e)|
+    silu = lambda t: t * torch.sigmoid(t)  # noqa: E731
+    v1 = torch.tensor([[0.02, -0.01, 0.03, 0.01], [0.01, 0.02, -0.02, 0.005]], dtype=torch.float64)
+    v2 = torch.tensor([[0.03, 0.01, -0.02, 0.02], [-0.01, 0.015, 0.02, 0.01]], dtype=torch.float64)
+    v3 = torch.tensor([[0.5, -0.5, 0.5, 0.5], [0.2, 0.1, 0.3, -0.4]], dtype=torch.float64)
+    z = torch.tensor([[[1.0, -1.0, 2.0, 0.5], [0.5, 1.0, -2.0, 3.0]],
+                      [[-0.5, 2.0, 1.0, 1.0], [1.0, 1.0, 1.0, 1.0]],
+                      [[2.0, 0.25, -1.0, 1.5], [-1.5, 0.5, 2.5, 1.0]]], dtype=torch.float64)
+    k_dirs = [e[0], e[1]]
+    q_rows = [[e[0], e[1]], [e[0], e[2]], [e[0], e[1]]]
+    v_rows = [v1, v2, v3]
+    ab = [(-30.0, 30.0), (-30.0, 30.0), (0.0, -30.0)]
+    rows = []
+    for t in range(3):
+        q = torch.cat([3.0 * q_rows[t][h] for h in range(heads)])
+        k = torch.cat([3.0 * k_dirs[h] for h in range(heads)])
+        rows.append(torch.cat([q, k, v_rows[t].reshape(-1), z[t].reshape(-1), torch.tensor([ab[t][0]] * heads,
+                    dtype=torch.float64), torch.tensor([ab[t][1]] * heads, dtype=torch.float64)]))
+    x = torch.stack(rows)
+    w_out = torch.tensor([1.0, 2.0, 0.5, 1.5], dtype=torch.float64)
+    conv = torch.zeros(3 * inner, 1, 4, dtype=torch.float64)
+    conv[:, 0, 3] = 1.0
+    weights = {"in_proj": torch.eye(x.shape[1], dtype=torch.float64), "conv": conv, "out_weight": w_out,
+               "A_log": torch.zeros(heads, dtype=torch.float64), "dt_bias": torch.zeros(heads, dtype=torch.float64),
+               "wo": torch.eye(inner, dtype=torch.float64)}
+    # closed forms: beta = sigmoid(30) and decay = exp(-softplus(-30)) are 1 to 1e-13; scale = 1/2
+    scale = hd**-0.5
+    half = torch.exp(-torch.log(torch.tensor(2.0, dtype=torch.float64)))  # exp(-softplus(0))
+    o = torch.zeros(3, heads, hd, dtype=torch.float64)
+    for h in range(heads):
+        o[0, h] = silu(v1[h]) * c * c * scale
+    o[1, 0] = silu(v2[0]) * c * c * scale  # q along k
+    o[1, 1] = 0.0  # q orthogonal to k
+    for h in range(heads):
+        o[2, h] = half * silu(v2[h]) * c * c * scale
+    y = o / torch.sqrt(o.pow(2).mean(-1, keepdim=True) + 1e-5) * w_out * silu(z)
+    state = torch.stack([half * torch.outer(silu(v2[h]), c * k_dirs[h]) for h in range(heads)])
+    history = x[:, : 3 * inner].T  # the last W-1 = 3 raw q|k|v inputs, oldest first
+    return x, weights, y.reshape(3, inner), state, history
+
+
+def _layer_variant(kind):
+    """gdn_layer's composition with one plausible mistake (its ops from the oracle's own parts)."""
+
+    def run(x, w, heads=2, head_dim=4, eps=1e-5):
+        hd, inner = head_dim, heads * head_dim
+        projection = F.linear(x, w["in_proj"])
+        qkv, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
+        if kind == "a_b_swapped":
+            aa, b = b, aa
+        conv, conv_state = O.causal_conv1d(qkv, w["conv"], None)
+        if kind == "no_conv_silu":
+            conv = F.silu(conv)  # a second SiLU stands for a misplaced one
+        q, k, v = [part.reshape(len(x), heads, hd).double() for part in conv.split(inner, -1)]
+        if kind == "q_k_swapped":
+            q, k = k, q
+        q = q * torch.rsqrt(q.square().sum(-1, keepdim=True) + 1e-6)
+        k = k * torch.rsqrt(k.square().sum(-1, keepdim=True) + 1e-6)
+        decay, beta = O.gate(aa, b, w["A_log"], w["dt_bias"])
+        o, state = O.gated_delta_sequence(q, k, v, decay.double(), beta.double(),
+                                          1.0 if kind == "no_scale" else hd**-0.5,
+                                          torch.zeros(heads, hd, hd, dtype=torch.float64))
+        o = o.double()
+        zz = z.reshape(len(x), heads, hd)
+        norm = o / torch.sqrt(o.pow(2).mean(-1, keepdim=True) + (1e-6 if kind == "eps_1e-6" else eps))
+        gate_z = zz if kind == "z_not_silu" else F.silu(zz)
+        return (norm * w["out_weight"] * gate_z).reshape(len(x), inner), state, conv_state
+
+    return run
+
+
+def test_layer_known_answer():
+    """gdn_layer against the hand-fixed answer of _kat_layer: outputs, final state and conv history."""
+    x, w, y_want, s_want, hist_want = _kat_layer()
+    y, conv_state, state, cap = O.gdn_layer(x, w, heads=2, head_dim=4)
+    # (gdn_layer runs the recurrence in float32, as lm.py:569 does: agreement to float32 rounding)
+    assert rel_err(y, y_want) < 1e-6, rel_err(y, y_want)
+    assert rel_err(state, s_want) < 1e-6
+    assert torch.equal(conv_state, hist_want)
+    assert rel_err(cap["gdn_gated"], y_want) < 1e-6  # wo = identity
+
+
+@pytest.mark.parametrize("kind", ["a_b_swapped", "eps_1e-6", "z_not_silu", "q_k_swapped", "no_conv_silu",
+                                  "no_scale"])
+def test_layer_planted_mistakes_fail_the_known_answer(kind):
+    x, w, y_want, s_want, _ = _kat_layer()
+    y, state, _ = _layer_variant("none")(x, w)
+    assert rel_err(y, y_want) < 1e-6 and rel_err(state, s_want) < 1e-6  # the unmutated composition passes
+    y, state, _ = _layer_variant(kind)(x, w)
+    assert rel_err(y, y_want) > 1e-3 or rel_err(state, s_want) > 1e-3, kind

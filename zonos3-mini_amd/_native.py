@@ -17,6 +17,8 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libzonos3_gdn.so"
 F32, BF16 = 0, 1
 # status codes (enum zgdn_status)
 OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
+# bits of the chunked path's device status word (zgdn_chunk_status)
+STATUS_WAIT_GAVE_UP = 1
 ABI_VERSION = 2  # zgdn_abi_version() of the library these signatures describe
 
 _P = c_void_p
@@ -32,6 +34,10 @@ SIGNATURES: dict[str, tuple] = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     ),
     "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
+    "zgdn_chunk_set_launch_form": (c_int, [c_int]),
+    "zgdn_chunk_get_launch_form": (c_int, []),
+    "zgdn_chunk_status": (c_int, [POINTER(c_int), c_int]),
+    "zgdn_chunk_set_wait_limit": (c_int, [c_int, c_int]),
     "zgdn_chunk_segment_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "zgdn_chunk_fwd": (
         c_int,

@@ -31,6 +31,7 @@
 // (kappa below) so that two 16 x 16 D tiles of W'^T computed in phase 1 are directly one A fragment.
 #include <type_traits>
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 
 #include "gdn_common.h"
@@ -130,7 +131,13 @@ __device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, cons
       r.len = 0;
       return r;
     }
-    const int bos = cu[s], eos = cu[s + 1];
+    int bos, eos;
+    seq_bounds(cu, s, T, bos, eos);
+    if (j >= (eos - bos + CH - 1) / CH) {  // past the sequence's chunks
+      r.t0 = 0;
+      r.len = 0;
+      return r;
+    }
     r.t0 = bos + j * CH;
     r.len = min(CH, eos - r.t0);
   } else {
@@ -717,14 +724,21 @@ struct StateArgs {
   int c0, bos, len, nchunks, Hv, h, vb;
   float xs;  // 1, or 0 for a transition run (Ub' and Ob taken as zero: the pass then carries S -> S A_c)
   // overlapped form: the ready flag of item (chunk c, head h) is flags[c * Hv + h], nonzero once phase 1
-  // has stored the item; err is set when a wait gives up
+  // has stored the item; spin_max bounds each wait (never_ready: every flag reads as unready, so each wait
+  // runs out -- the host's test of the error path)
   int* flags;
-  int* err;
+  int spin_max;
+  int never_ready;
 };
 
-// Bound on a state pass's wait for one item (a few tenths of a second): a wait that runs out records an error,
-// and the wave then waits no more, so that every wave of the kernel ends soon.
+// Default bound on a state pass's wait for one item (a few tenths of a second): a wait that runs out sets bit
+// ZGDN_STATUS_WAIT_GAVE_UP of the device status word, and the wave then waits no more, so that every wave of
+// the kernel ends soon.
 constexpr int SPIN_MAX = 1 << 17;
+
+// Sticky device status of this library's chunked-prefill kernels on each device (bits of zgdn_chunk_status),
+// read and cleared by zgdn_chunk_status.
+__device__ int g_chunk_status;
 
 __device__ __forceinline__ int load_flag(const int* f) {
   return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -806,16 +820,18 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     if constexpr (Wait) {
       int f = gave_up ? 1 : fl;
       for (int n = 0; f == 0; ++n) {
-        if (n == SPIN_MAX) {
-          if (l == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (n >= a.spin_max) {
+          if (l == 0)
+            __hip_atomic_fetch_or(&g_chunk_status, ZGDN_STATUS_WAIT_GAVE_UP, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
           gave_up = true;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
-        f = load_flag(fbase + (size_t)ni * a.Hv);
+        f = a.never_ready ? 0 : load_flag(fbase + (size_t)ni * a.Hv);
       }
       asm volatile("" ::: "memory");  // the chunk's loads stay behind the wait
-      fl = load_flag(fbase + (size_t)min(ni + 1, last) * a.Hv);
+      fl = a.never_ready ? 0 : load_flag(fbase + (size_t)min(ni + 1, last) * a.Hv);
     }
   };
 
@@ -937,10 +953,15 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   a.vb = vb;
   a.xs = trans ? 0.f : 1.f;
   if (cu != nullptr) {  // packed sequences: plain runs only
-    a.bos = cu[seq];
-    a.len = cu[seq + 1] - a.bos;
+    int eos;
+    seq_bounds(cu, seq, T, a.bos, eos);
+    a.len = eos - a.bos;
     a.c0 = 0;
-    for (int s = 0; s < seq; ++s) a.c0 += (cu[s + 1] - cu[s] + CH - 1) / CH;
+    for (int s = 0; s < seq; ++s) {
+      int sb, se;
+      seq_bounds(cu, s, T, sb, se);
+      a.c0 += (se - sb + CH - 1) / CH;
+    }
   } else {
     const int nct = (T + CH - 1) / CH;
     a.bos = seq * T + sg * seg.Cs * CH;
@@ -966,7 +987,8 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 
   TOut* out = trans ? reinterpret_cast<TOut*>(seg.trans_out) : o;
   a.flags = nullptr;
-  a.err = nullptr;
+  a.spin_max = 0;
+  a.never_ready = 0;
   if (wave < 4)
     state_loop<true, TOut, false>(sh, a, out, S);
   else
@@ -1013,8 +1035,8 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 //   many chains: the first arrival takes items, the next FQ_STATE_WORKERS state jobs one after another, the
 //     rest items; items chain after chain, so state jobs start in the order their chains are produced.
 // Progress: items never wait and every queue's first arrival takes items, so every item is stored whatever the
-// number of resident workgroups; a wait that runs out (SPIN_MAX) records an error and the kernel still ends.
-// The control block (per-queue tickets, the error word, one flag per item) is zeroed before each launch.
+// number of resident workgroups; a wait that runs out (the spin bound) sets the device status word and the kernel still ends.
+// The control block (per-queue tickets, one flag per item) is zeroed before each launch.
 constexpr int FQ_MAX = 8;              // queues (one per XCD)
 constexpr int FQ_FEW_CHAINS = 4;       // chains per queue of the few-chains order (32 state workgroups of 64)
 constexpr int FQ_STATE_WORKERS = 24;   // workgroups per queue taking state jobs in the many-chains order
@@ -1023,13 +1045,14 @@ constexpr int FQ_MAX_QCHAINS = 512;    // chains per queue in the many-chains or
 
 struct FusedCtl {
   int* tickets;  // queue q: role ticket at [96 q], item ticket at [96 q + 32], state ticket at [96 q + 64]
-  int* err;
   int* flags;    // [n_items]
   int n_q;       // queues in use (XCDs of the device)
   int few;       // few-chains order
+  int spin_max;  // bound of each wait for a ready flag
+  int never_ready;
 };
 
-constexpr size_t FQ_HEADER = 256 * 13;  // tickets (8 queues x 3 lines of 128 bytes), error word
+constexpr size_t FQ_HEADER = 256 * 13;  // tickets (8 queues x 3 lines of 128 bytes), then padding
 size_t fused_ctl_bytes(int n_items) { return FQ_HEADER + (((size_t)n_items * 4 + 255) / 256) * 256; }
 
 __global__ void zero_ints_kernel(int* p, int n) {
@@ -1082,14 +1105,24 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
   const int nch = (n_chains - qi + ctl.n_q - 1) / ctl.n_q;  // chains of this queue: qi + n_q m, m < nch
   const int n_state = nch * (DV / VB);
   const int n_items = n_chunks * Hv;
-  auto seq_bos = [&](int sq) { return cu != nullptr ? cu[sq] : sq * T; };
-  auto seq_len = [&](int sq) { return cu != nullptr ? cu[sq + 1] - cu[sq] : T; };
+  auto seq_bos = [&](int sq) {
+    if (cu == nullptr) return sq * T;
+    int sb, se;
+    seq_bounds(cu, sq, T, sb, se);
+    return sb;
+  };
+  auto seq_len = [&](int sq) {
+    if (cu == nullptr) return T;
+    int sb, se;
+    seq_bounds(cu, sq, T, sb, se);
+    return se - sb;
+  };
 
   // tables of the many-chains order
   if (!ctl.few) {
     if (cu != nullptr) {
       const int t = threadIdx.x;
-      block_exclusive_scan(t < n_seqs ? (cu[t + 1] - cu[t] + CH - 1) / CH : 0, n_seqs, seq_c0, wsum);
+      block_exclusive_scan(t < n_seqs ? (seq_len(t) + CH - 1) / CH : 0, n_seqs, seq_c0, wsum);
     }
     const int t = threadIdx.x;
     int len = 0;
@@ -1132,7 +1165,8 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
       a.c0 = chunk0(sq);
       a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
       a.flags = ctl.flags;
-      a.err = ctl.err;
+      a.spin_max = ctl.spin_max;
+      a.never_ready = ctl.never_ready;
       const int ncol = 16 * wave + (l & 15);
       const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
       const size_t hs = (size_t)DV * DK;
@@ -1376,7 +1410,7 @@ SegPlan seg_plan(int B, int T, int Hv, int n_cu) {
   const int nct = (T + CH - 1) / CH;
   const long base = (long)B * Hv * (DV / VB);
   SegPlan p{1, nct};
-  if (2 * base > n_cu) return p;
+  if (nct < 8 || 2 * base > n_cu) return p;  // (a segment holds at least 4 chunks)
   long best = 64L * nct;
   for (int g = 2; g <= 8; ++g) {
     const int cs = (nct + g - 1) / g, gg = (nct + cs - 1) / cs;
@@ -1398,8 +1432,22 @@ size_t seg_bytes(int B, int T, int Hv, const SegPlan& p) {
   return (size_t)B * T * Hv * DK * 2 + (size_t)B * Hv * hs * (4 * p.G + 4 * (p.G - 1) + 2 * (p.G - 1));
 }
 
-// Whether an eligible batch takes the overlapped launch. ZGDN_CHUNK_OVERLAP in the environment (read at each
-// call) forces it off ("0") or on ("1"); otherwise it is taken where it measured faster than the two launches
+// Launch form of the chunked path: -1 the library's choice, 0 always two launches, 1 the overlapped launch for
+// every eligible batch. Set by zgdn_chunk_set_launch_form; its initial value comes from ZGDN_CHUNK_OVERLAP
+// ("0" / "1"), read once when the library is loaded, so that no call reads the environment.
+int launch_form_from_env() {
+  const char* e = std::getenv("ZGDN_CHUNK_OVERLAP");
+  if (e != nullptr && e[0] == '0') return 0;
+  if (e != nullptr && e[0] == '1') return 1;
+  return -1;
+}
+std::atomic<int> g_launch_form{launch_form_from_env()};
+// Spin bound of the overlapped launch's waits and the never-ready test switch (zgdn_chunk_set_wait_limit).
+std::atomic<int> g_spin_max{SPIN_MAX};
+std::atomic<int> g_never_ready{0};
+
+// Whether an eligible batch takes the overlapped launch: as the launch form says, or (the library's choice)
+// where it measured faster than the two launches
 // on MI355X (same-process comparisons, bf16, dk = dv = 128): few chains only with long sequences (64 chunks:
 // 82.6 against 84.6 us; at 8 .. 32 chunks it was 15-45 % slower), many chains when there are at least 3072
 // chunk x head items and 8 chunks or more per chain on average (+3-11 %: 512 chains of 8 chunks, 256 of 12 or
@@ -1407,9 +1455,9 @@ size_t seg_bytes(int B, int T, int Hv, const SegPlan& p) {
 // pass starts only after the first items, shares its CUs with phase 1, and with a fixed share of state
 // workgroups short or few chains leave them waiting).
 bool overlap_wanted(bool few, long n_items, double chunks_per_chain) {
-  const char* e = std::getenv("ZGDN_CHUNK_OVERLAP");
-  if (e != nullptr && e[0] == '0') return false;
-  if (e != nullptr && e[0] == '1') return true;
+  const int form = g_launch_form.load(std::memory_order_relaxed);
+  if (form == 0) return false;
+  if (form == 1) return true;
   if (few) return chunks_per_chain >= 64;
   return n_items >= 3072 && chunks_per_chain >= 8;
 }
@@ -1445,6 +1493,34 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
 }  // namespace
 }  // namespace zgdn
 
+extern "C" int zgdn_chunk_set_launch_form(int form) {
+  if (form < -1 || form > 1) return zgdn::fail(ZGDN_EINVAL, "zgdn_chunk_set_launch_form: form %d (-1, 0 or 1)", form);
+  zgdn::g_launch_form.store(form);
+  return ZGDN_OK;
+}
+
+extern "C" int zgdn_chunk_get_launch_form(void) { return zgdn::g_launch_form.load(); }
+
+extern "C" int zgdn_chunk_set_wait_limit(int spins, int never_ready) {
+  if (spins < 0) return zgdn::fail(ZGDN_EINVAL, "zgdn_chunk_set_wait_limit: spins %d", spins);
+  zgdn::g_spin_max.store(spins == 0 ? zgdn::SPIN_MAX : spins);
+  zgdn::g_never_ready.store(never_ready != 0);
+  return ZGDN_OK;
+}
+
+extern "C" int zgdn_chunk_status(int* status, int clear) {
+  if (status == nullptr) return zgdn::fail(ZGDN_EINVAL, "zgdn_chunk_status: null pointer");
+  *status = 0;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(status, HIP_SYMBOL(zgdn::g_chunk_status), sizeof(int));
+  if (e == hipSuccess && clear) {
+    const int zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(zgdn::g_chunk_status), &zero, sizeof(int));
+  }
+  if (e != hipSuccess) return zgdn::fail(ZGDN_EHIP, "zgdn_chunk_status: %s", hipGetErrorString(e));
+  return ZGDN_OK;
+}
+
 extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
   const size_t items = (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0);
   return items * zgdn::WS_CHUNK + zgdn::fused_ctl_bytes((int)items);
@@ -1465,7 +1541,9 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
                               void* stream) {
   using namespace zgdn;
   const char* fn = "zgdn_chunk_fwd";
-  if (!q || !k || !v || !g || !beta || !o || !workspace) return fail(ZGDN_EINVAL, "%s: null pointer", fn);
+  // (with no tokens, T == 0, the token arrays may be empty allocations: only the states are touched)
+  if (!workspace || (T > 0 && (!q || !k || !v || !g || !beta || !o)))
+    return fail(ZGDN_EINVAL, "%s: null pointer", fn);
   if (K != DK || V != DV) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d V=%d (supported: 128, 128)", fn, K, V);
   if (qkv_dtype != ZGDN_BF16) return fail(ZGDN_EUNSUPPORTED, "%s: q/k/v must be bf16", fn);
   if (gb_dtype != ZGDN_F32 && gb_dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, gb_dtype);
@@ -1526,7 +1604,8 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
       overlap_wanted(few, (long)n_chunks * Hv, (double)n_chunks / std::max(1, N))) {
     const int n_items = n_chunks * Hv;
     int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
-    const FusedCtl ctl{ctl_base, ctl_base + 96 * FQ_MAX, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0};
+    const FusedCtl ctl{ctl_base, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0,
+                       g_spin_max.load(std::memory_order_relaxed), g_never_ready.load(std::memory_order_relaxed)};
     const int n_ctl = (int)(fused_ctl_bytes(n_items) / 4);
     hipLaunchKernelGGL(zero_ints_kernel, dim3((n_ctl + 255) / 256), dim3(256), 0, s, ctl_base, n_ctl);
     const dim3 grid(P1_WGS_PER_CU * device_cus());

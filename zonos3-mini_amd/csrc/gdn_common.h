@@ -86,6 +86,16 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------------------- packed sequences
+
+// Token range [bos, eos) of packed sequence s (cu_seqlens int32 [n + 1]), clamped into [0, T]: a table that
+// decreases or runs past the T tokens of the batch gives empty or shortened ranges, so no kernel reads or
+// writes a token row outside the batch. (The host layer rejects such tables wherever it holds them.)
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int T, int& bos, int& eos) {
+  bos = min(max(cu[s], 0), T);
+  eos = min(max(cu[s + 1], bos), T);
+}
+
 // -------------------------------------------------------------------------------------------------- math
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }

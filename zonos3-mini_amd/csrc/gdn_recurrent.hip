@@ -52,8 +52,7 @@ __global__ __launch_bounds__(64 * NWAVES) void recurrent_kernel(
   const int hk = h / (Hv / Hk);
   int bos, eos;
   if (cu != nullptr) {
-    bos = cu[n];
-    eos = cu[n + 1];
+    seq_bounds(cu, n, T, bos, eos);
   } else {
     bos = n * T;
     eos = bos + T;

@@ -81,7 +81,9 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
     // trailing workgroups, one per sequence: empty packed sequences pass their state row through (zeros
     // without one)
     seq = blockIdx.x - n_chunks * CONV_SPLIT;
-    if (fin == nullptr || cu[seq + 1] != cu[seq]) return;
+    int sb, se;
+    seq_bounds(cu, seq, T_len, sb, se);
+    if (fin == nullptr || se != sb) return;
     for (int k = 0; k < CPT; ++k) {
       T* frow = fin + ((size_t)seq * D + c0 + k) * SW;
       const T* hrow = init != nullptr ? init + ((size_t)seq * D + c0 + k) * SW : nullptr;
@@ -98,10 +100,12 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
     seq = tile / nt;
     j = tile % nt;
   }
-  const int bos = cu != nullptr ? cu[seq] : seq * T_len;
-  const int len = cu != nullptr ? cu[seq + 1] - bos : T_len;
-  const int t0 = j * CONV_CH + sub * CONV_TT;
-  const int t1 = min(len, t0 + CONV_TT);
+  int bos = seq * T_len, len = T_len;
+  if (cu != nullptr) {
+    int eos;
+    seq_bounds(cu, seq, T_len, bos, eos);
+    len = eos - bos;
+  }
   const bool writes_state = fin != nullptr && j == 0 && sub == 0;
   if (len == 0) {  // an empty sequence (a batch of T = 0) passes its state row through
     if (writes_state)
@@ -112,6 +116,9 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_kernel(
       }
     return;
   }
+  if (j >= (len + CONV_CH - 1) / CONV_CH) return;  // a table row past the sequence's chunks
+  const int t0 = j * CONV_CH + sub * CONV_TT;
+  const int t1 = min(len, t0 + CONV_TT);
   if (t0 >= len) return;
 
   // Every load below is unconditional (indices clamped into the sequence / state row, a missing state row

@@ -9,6 +9,7 @@ without synchronising the host, so every call can be captured into a HIP graph. 
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -41,6 +42,11 @@ def _row_stride(t: torch.Tensor, inner_dims: int) -> int | None:
     leading dims step in whole rows (a column slice of a wider row-major buffer qualifies); None otherwise."""
     shape, stride = t.shape, t.stride()
     lead = t.dim() - inner_dims
+    if t.numel() == 0:  # no rows to read: any stride will do
+        w = 1
+        for n in shape[lead:]:
+            w *= n
+        return w
     width = 1
     for d in range(t.dim() - 1, lead - 1, -1):
         if shape[d] != 1 and stride[d] != width:
@@ -104,11 +110,63 @@ def _gate_check(A_log, dt_bias, Hv: int, device) -> None:
             _require(t.dtype == torch.float32 and t.shape == (Hv,), f"{name}: expected float32 [{Hv}]")
 
 
+def check_cu_seqlens(cu: list[int], total: int) -> None:
+    """Raise RuntimeError unless ``cu`` (host values of cu_seqlens) starts at 0, never decreases and ends at
+    ``total`` tokens -- the packed-length checks the serving layer makes before any launch
+    (``servers/sgl/src/zonos3_sgl/models/gdn.py:247-255``; empty sequences are allowed here, as FLA's tables
+    allow them)."""
+    _require(len(cu) >= 2, f"cu_seqlens: {len(cu)} entries, need at least 2")
+    _require(cu[0] == 0, f"cu_seqlens: starts at {cu[0]}, expected 0")
+    for i in range(len(cu) - 1):
+        _require(cu[i + 1] >= cu[i], f"cu_seqlens: decreases at entry {i} ({cu[i]} -> {cu[i + 1]})")
+    _require(cu[-1] == total, f"cu_seqlens: ends at {cu[-1]}, but the batch holds {total} tokens")
+
+
+def _table_rows(cu: list[int]) -> list[tuple[int, int]]:
+    return [(i, j) for i in range(len(cu) - 1) for j in range(-(-(cu[i + 1] - cu[i]) // CHUNK))]
+
+
+def check_chunk_indices(rows, cu: list[int]) -> None:
+    """Raise RuntimeError unless ``rows`` (host values of the [n_chunks, 2] chunk table) is exactly the
+    (sequence, chunk within it) table of ``gdn.py:49-59`` for the sequences of ``cu``."""
+    expect = _table_rows(cu)
+    got = [tuple(int(x) for x in r) for r in rows]
+    if got != expect:
+        first = next((i for i, (a, b) in enumerate(zip(got, expect)) if a != b), min(len(got), len(expect)))
+        raise RuntimeError(f"chunk_indices: {len(got)} rows do not match the {len(expect)} chunks of cu_seqlens "
+                           f"(first difference at row {first})")
+
+
 def _cu_check(cu_seqlens: torch.Tensor, total: int, device) -> int:
+    """Type checks of a device cu_seqlens. Its values stay on the device (no host read, so the call can be
+    captured into a graph); the kernels clamp each sequence's token range into the batch, so a malformed
+    device table cannot make them touch rows outside it."""
     _on_gpu("cu_seqlens", cu_seqlens, device)
     _require(cu_seqlens.dtype == torch.int32, "cu_seqlens: must be int32")
     _require(cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 2, "cu_seqlens: must be 1-D with >= 2 entries")
     return cu_seqlens.numel() - 1
+
+
+def _on_host(t) -> bool:
+    return t is not None and (not isinstance(t, torch.Tensor) or not t.is_cuda)
+
+
+def host_tables(cu_seqlens, chunk_indices, total: int, device=None):
+    """Packed tables held on the host (lists or CPU tensors), as the reference builds them (gdn.py:49-59):
+    checked (``check_cu_seqlens``, ``check_chunk_indices``; the chunk table is built when None), then copied
+    to ``device`` in one transfer. Returns int32 (cu_seqlens [N+1], chunk_indices [n_chunks, 2]); raises
+    RuntimeError before any copy or launch when a table is malformed."""
+    cu = cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else [int(x) for x in cu_seqlens]
+    check_cu_seqlens(cu, total)
+    if chunk_indices is None:
+        rows = _table_rows(cu)
+    else:
+        rows = chunk_indices.tolist() if isinstance(chunk_indices, torch.Tensor) else list(chunk_indices)
+        check_chunk_indices(rows, cu)
+    flat = torch.tensor(cu + [int(x) for r in rows for x in r], dtype=torch.int32)
+    if device is not None:
+        flat = flat.to(device)
+    return flat[: len(cu)], flat[len(cu):].view(-1, 2)
 
 
 def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
@@ -139,6 +197,8 @@ def recurrent_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final
     n_seqs = B
     if cu_seqlens is not None:
         _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        if _on_host(cu_seqlens):  # a host table: checked here, then copied
+            cu_seqlens, _ = host_tables(cu_seqlens, None, T, dev)
         n_seqs = _cu_check(cu_seqlens, T, dev)
     if initial_state is not None:
         _on_gpu("initial_state", initial_state, dev)
@@ -175,14 +235,57 @@ def decode_step(q, k, v, g, beta, state, scale=None):
 CHUNK = 64  # chunk length of the chunked kernels (servers/sgl/src/zonos3_sgl/models/gdn.py:46)
 
 
-def chunk_indices_from_cu(cu_seqlens: torch.Tensor) -> torch.Tensor:
+def chunk_indices_from_cu(cu_seqlens: torch.Tensor, total: int | None = None) -> torch.Tensor:
     """(sequence, chunk within it) int32 [n_chunks, 2] of packed sequences (gdn.py:49-59). Reads
-    ``cu_seqlens`` on the host (one device->host copy); callers that already hold the lengths on the host
-    build the table there, as the reference does."""
+    ``cu_seqlens`` on the host (one device->host copy) and checks it there (``check_cu_seqlens``, against
+    ``total`` tokens when given); callers that already hold the lengths on the host build the table there, as
+    the reference does."""
     cu = cu_seqlens.tolist()
-    rows = [(i, j) for i in range(len(cu) - 1) for j in range(-(-(cu[i + 1] - cu[i]) // CHUNK))]
-    t = torch.tensor(rows, dtype=torch.int32).reshape(-1, 2)
+    check_cu_seqlens(cu, cu[-1] if total is None and cu else total)
+    t = torch.tensor(_table_rows(cu), dtype=torch.int32).reshape(-1, 2)
     return t.to(cu_seqlens.device)
+
+
+class launch_form:
+    """Context manager setting the chunked path's launch form for the process (``zgdn_chunk_set_launch_form``:
+    -1 the library's choice, 0 two launches, 1 the overlapped launch wherever eligible) and restoring the
+    previous form on exit. Every form gives the same results bit for bit."""
+
+    def __init__(self, form: int):
+        self.form = int(form)
+        self.prev = None
+
+    def __enter__(self):
+        self.prev = int(_native.lib().zgdn_chunk_get_launch_form())
+        _native.call("zgdn_chunk_set_launch_form", self.form)
+        return self
+
+    def __exit__(self, *exc):
+        _native.call("zgdn_chunk_set_launch_form", self.prev)
+        return False
+
+
+def chunk_status(clear: bool = True) -> int:
+    """Bits of the chunked path's sticky device status word (0 = no error): ``_native.STATUS_WAIT_GAVE_UP``
+    when an overlapped launch's bounded wait ran out, leaving that call's outputs undefined. Synchronises the
+    device; ``clear`` resets the word."""
+    out = ctypes.c_int(0)
+    _native.call("zgdn_chunk_status", ctypes.byref(out), int(bool(clear)))
+    return out.value
+
+
+def check_chunk_status() -> None:
+    """Raise RuntimeError when the chunked path's device status word records an error (and clear it)."""
+    st = chunk_status(clear=True)
+    if st:
+        raise RuntimeError(f"chunked prefill: device status {st:#x} (a state pass gave up waiting for its chunk's "
+                           "phase-1 results; the outputs and final states of that call are undefined)")
+
+
+# Validation mode (ZGDN_VALIDATE=1 in the environment, read once at import): every chunk_fwd then synchronises
+# the device after its launch and raises RuntimeError when the device status word records an error. Off by
+# default, so that calls stay asynchronous and capturable.
+VALIDATE = os.environ.get("ZGDN_VALIDATE", "0") not in ("", "0")
 
 
 def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
@@ -225,9 +328,11 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     n_chunks = B * (-(-T // CHUNK))
     if cu_seqlens is not None:
         _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        if _on_host(cu_seqlens):  # host tables: checked here, then copied
+            cu_seqlens, chunk_indices = host_tables(cu_seqlens, chunk_indices, T, dev)
         n_seqs = _cu_check(cu_seqlens, T, dev)
         if chunk_indices is None:
-            chunk_indices = chunk_indices_from_cu(cu_seqlens)
+            chunk_indices = chunk_indices_from_cu(cu_seqlens, T)
         _on_gpu("chunk_indices", chunk_indices, dev)
         _require(chunk_indices.dtype == torch.int32 and chunk_indices.dim() == 2 and chunk_indices.shape[1] == 2,
                  "chunk_indices: expected int32 [n_chunks, 2]")
@@ -257,6 +362,8 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
         _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, q_ld, k_ld, v_ld, gb_ld, int(bool(beta_is_logit)),
         scale, workspace.data_ptr(), ws_bytes, _stream(dev),
     )
+    if VALIDATE:
+        check_chunk_status()
     return o, final_state
 
 
@@ -436,9 +543,11 @@ def causal_conv1d(x, weight, bias=None, initial_state=None, output_final_state=T
     n_seqs, n_chunks = B, 0
     if cu_seqlens is not None:
         _require(B == 1, "cu_seqlens: packed sequences need B == 1")
+        if _on_host(cu_seqlens):  # host tables: checked here, then copied
+            cu_seqlens, chunk_indices = host_tables(cu_seqlens, chunk_indices, T, dev)
         n_seqs = _cu_check(cu_seqlens, T, dev)
         if chunk_indices is None:
-            chunk_indices = chunk_indices_from_cu(cu_seqlens)
+            chunk_indices = chunk_indices_from_cu(cu_seqlens, T)
         _on_gpu("chunk_indices", chunk_indices, dev)
         _require(chunk_indices.dtype == torch.int32 and chunk_indices.dim() == 2 and chunk_indices.shape[1] == 2,
                  "chunk_indices: expected int32 [n_chunks, 2]")
