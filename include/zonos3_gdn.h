@@ -132,6 +132,27 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * zgdn_chunk_fwd without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: FLA's
+ * chunk_gated_delta_rule_fwd allocates its own intermediates. Same arguments, layouts and results as
+ * zgdn_chunk_fwd (the same kernels); the caller still passes every input and output. The workspace is the
+ * library's own per-device scratch of zgdn_chunk_noalloc_max_bytes() bytes (64 MiB: 680 chunk x head items,
+ * e.g. 4 heads up to 10,880 tokens or 16 heads up to 2,720), a static device array held by each device the
+ * library runs on until the process ends; calls needing more fail with ZGDN_EINVAL before any launch. Its
+ * address is looked up once per device (hipGetSymbolAddress, with the device current), then no call
+ * allocates. Every call on one device shares that device's scratch, which keeps the last call's contents (the
+ * kernels clear what must start at zero with a fill kernel): calls that overlap on one device, e.g. on two
+ * streams, race and must be serialised by the caller.
+ */
+size_t zgdn_chunk_noalloc_max_bytes(void);
+int zgdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                           const void* beta, int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
+                           const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
+                           const int32_t* chunk_indices, int n_seqs, int n_chunks, int B, int T, int Hk, int Hv,
+                           int K, int V, long q_ld, long k_ld, long v_ld, long gb_ld, int beta_sigmoid, float scale,
+                           void* stream);
+
+/*
  * One single-token step of the whole GDN block for B independent streams, fused in one launch: depthwise
  * causal conv1d (width W == 4) over the raw q|k|v channels with a rolling history, SiLU, q/k L2-norm, the
  * in-kernel gate, the gated delta-rule state update and the gated RMSNorm of the output. Replaces, for one

@@ -25,7 +25,8 @@ def test_header_declares_entry_points():
             "zgdn_fused_decode_step", "zgdn_causal_conv1d_fwd", "zgdn_l2norm_fwd", "zgdn_sigmoid_fwd",
             "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route", "zgdn_accent_workspace_size",
             "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size", "zgdn_chunk_set_launch_form",
-            "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit"} == _declared()
+            "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit",
+            "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):

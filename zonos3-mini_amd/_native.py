@@ -45,6 +45,12 @@ SIGNATURES: dict[str, tuple] = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_long, c_int, c_float, _P, c_size_t,
          _P],
     ),
+    "zgdn_chunk_noalloc_max_bytes": (c_size_t, []),
+    "zgdn_chunk_fwd_noalloc": (
+        c_int,
+        [_P, _P, _P, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int,
+         c_int, c_int, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_long, c_int, c_float, _P],
+    ),
     "zgdn_fused_decode_step": (
         c_int,
         [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P,

@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "gdn_common.h"
 
@@ -1532,15 +1533,15 @@ extern "C" size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv) {
   return seg_bytes(B, T, Hv, seg_plan(B, T, Hv, device_cus()));
 }
 
-extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
-                              const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
-                              int qk_l2norm, const float* initial_state, float* final_state, void* o,
-                              const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
-                              int B, int T, int Hk, int Hv, int K, int V, long q_ld, long k_ld, long v_ld,
-                              long gb_ld, int beta_sigmoid, float scale, void* workspace, size_t workspace_bytes,
-                              void* stream) {
-  using namespace zgdn;
-  const char* fn = "zgdn_chunk_fwd";
+namespace zgdn {
+namespace {
+// The chunked forward behind zgdn_chunk_fwd and zgdn_chunk_fwd_noalloc (`fn` names the entry in messages).
+int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                   const void* beta, int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
+                   const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
+                   const int32_t* chunk_indices, int n_seqs, int n_chunks, int B, int T, int Hk, int Hv, int K,
+                   int V, long q_ld, long k_ld, long v_ld, long gb_ld, int beta_sigmoid, float scale,
+                   void* workspace, size_t workspace_bytes, void* stream) {
   // (with no tokens, T == 0, the token arrays may be empty allocations: only the states are touched)
   if (!workspace || (T > 0 && (!q || !k || !v || !g || !beta || !o)))
     return fail(ZGDN_EINVAL, "%s: null pointer", fn);
@@ -1643,4 +1644,87 @@ extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int q
                        run.trans_out, (bf16*)o, T, Hv, run.G, run.Cs);
   }
   return check_launch(fn);
+}
+
+// Scratch of zgdn_chunk_fwd_noalloc: the chunked path's workspace in a file-scope device array, one copy per
+// device, allocated when the library's code object is loaded on that device and held until the process ends.
+// Host code never passes the array's name to a kernel (that is a host-side stand-in, not a device address): it
+// uses the address hipGetSymbolAddress returns for the current device, obtained once per device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// The scratch's device address on the current device (looked up on the first call per device); nullptr with a
+// recorded error on failure.
+void* scratch_on_current_device(const char* fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(ZGDN_EHIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    fail(ZGDN_EUNSUPPORTED, "%s: device %d (supported: 0 .. %d)", fn, dev, NOALLOC_MAX_DEVICES - 1);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      fail(ZGDN_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+           e != hipSuccess ? hipGetErrorString(e) : "null address");
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+}  // namespace zgdn
+
+extern "C" int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                              const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
+                              int qk_l2norm, const float* initial_state, float* final_state, void* o,
+                              const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs, int n_chunks,
+                              int B, int T, int Hk, int Hv, int K, int V, long q_ld, long k_ld, long v_ld,
+                              long gb_ld, int beta_sigmoid, float scale, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return zgdn::chunk_fwd_impl("zgdn_chunk_fwd", q, k, v, qkv_dtype, g, beta, gb_dtype, A_log, dt_bias, qk_l2norm,
+                              initial_state, final_state, o, cu_seqlens, chunk_indices, n_seqs, n_chunks, B, T, Hk,
+                              Hv, K, V, q_ld, k_ld, v_ld, gb_ld, beta_sigmoid, scale, workspace, workspace_bytes,
+                              stream);
+}
+
+extern "C" size_t zgdn_chunk_noalloc_max_bytes(void) { return zgdn::NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int zgdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                                      const void* beta, int gb_dtype, const float* A_log, const float* dt_bias,
+                                      int qk_l2norm, const float* initial_state, float* final_state, void* o,
+                                      const int32_t* cu_seqlens, const int32_t* chunk_indices, int n_seqs,
+                                      int n_chunks, int B, int T, int Hk, int Hv, int K, int V, long q_ld, long k_ld,
+                                      long v_ld, long gb_ld, int beta_sigmoid, float scale, void* stream) {
+  using namespace zgdn;
+  const char* fn = "zgdn_chunk_fwd_noalloc";
+  const int nc = cu_seqlens != nullptr ? n_chunks : (B > 0 && T >= 0 ? B * ((T + CH - 1) / CH) : 0);
+  if (nc < 0 || Hv < 1) return fail(ZGDN_EINVAL, "%s: n_chunks=%d Hv=%d", fn, nc, Hv);
+  const size_t need = zgdn_chunk_workspace_size(nc, Hv);
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(ZGDN_EINVAL, "%s: %d chunks x %d heads need %zu bytes of workspace, above the %zu-byte scratch "
+                "of this entry point (use zgdn_chunk_fwd with a caller workspace)", fn, nc, Hv, need,
+                NOALLOC_SCRATCH_BYTES);
+  void* ptr = scratch_on_current_device(fn);
+  if (ptr == nullptr) return ZGDN_EHIP;
+  // the segmented state pass's extra space when it fits the scratch as well, else the plain pass
+  size_t bytes = need;
+  if (cu_seqlens == nullptr && B > 0 && T > 0) {
+    const size_t seg = zgdn_chunk_segment_workspace_size(B, T, Hv);
+    if (seg > 0 && need + seg <= NOALLOC_SCRATCH_BYTES) bytes = need + seg;
+  }
+  return chunk_fwd_impl(fn, q, k, v, qkv_dtype, g, beta, gb_dtype, A_log, dt_bias, qk_l2norm, initial_state,
+                        final_state, o, cu_seqlens, chunk_indices, n_seqs, n_chunks, B, T, Hk, Hv, K, V, q_ld,
+                        k_ld, v_ld, gb_ld, beta_sigmoid, scale, ptr, bytes, stream);
 }
