@@ -71,22 +71,22 @@ def test_eager_path_rejects_bad_batches_before_any_kernel(serving):
     with pytest.raises(RuntimeError, match="already allocated"):
         layer.allocate_cache(4, torch.device("cpu"), torch.float32)
     cases = [
-        ([_req(0, 0, 3), _req(0, 0, 2)], 5, "slots or packed lengths"),  # the same slot twice
-        ([_req(0, 0, 3), _req(4, 0, 2)], 5, "slots or packed lengths"),  # slot outside the cache
-        ([_req(0, 0, 3), _req(1, 0, 0)], 3, "slots or packed lengths"),  # an empty request
-        ([_req(0, 0, 3), _req(1, 0, 2)], 6, "slots or packed lengths"),  # rows != sum of lengths
-        ([_req(0, 7, 1)], 1, "missing/stale state at slot 0"),  # no state for a cached prefix
+        ([_req(0, 0, 3), _req(0, 0, 2)], 5, "slot 0 named by two requests"),
+        ([_req(0, 0, 3), _req(4, 0, 2)], 5, "slot 4 outside the 4 slots"),
+        ([_req(0, 0, 3), _req(1, 0, 0)], 3, "slot 1 brings 0 rows"),
+        ([_req(0, 0, 3), _req(1, 0, 2)], 6, "6 rows given for requests of 5 rows"),
+        ([_req(0, 7, 1)], 1, r"slot 0 has no state for \(0, False\) at row 7"),  # a cached prefix, no state
     ]
     for reqs, rows, message in cases:
         batch.reqs = batch.padded_reqs = reqs
         with pytest.raises(RuntimeError, match=message):
             layer.forward(torch.zeros(rows, 32))
     batch.reqs, batch.padded_reqs = [_req(0, 0, 1)], [_req(0, 0, 1), _req(1, 0, 1)]
-    with pytest.raises(RuntimeError, match="dummy graph-padding"):
+    with pytest.raises(RuntimeError, match="1 dummy graph-padding requests"):
         layer.forward(torch.zeros(1, 32))
     batch.is_decode = True
     batch.reqs = batch.padded_reqs = [_req(0, 0, 2)]
-    with pytest.raises(RuntimeError, match="one new token"):
+    with pytest.raises(RuntimeError, match="one new row per request, slot 0 has 2"):
         layer.forward(torch.zeros(2, 32))
     layer.set_static_mode(True)
     with pytest.raises(RuntimeError, match="not prepared for batch size 2"):
@@ -94,3 +94,100 @@ def test_eager_path_rejects_bad_batches_before_any_kernel(serving):
     assert layer._owners == [None] * 4 and not layer._win_len.any()  # nothing was changed
     with pytest.raises(RuntimeError, match="batch source"):
         serving.OriginalGDN(SimpleNamespace(hidden_size=32), 0).forward(torch.zeros(1, 32))
+
+
+def _transparent_packed(calls):
+    """A stand-in for ``_run_packed`` on the CPU that makes the bookkeeping visible: output row = input row +
+    its position in its packed sequence; conv / recurrent final = initial + the sum of the sequence's rows
+    (so a slot's states telescope to the sum of the rows that went through them). Checks the chunk tables
+    against the sequence lengths."""
+
+    def run(x, cu, chunks, conv, recurrent, mask=None, valid=None, return_mixed=False):
+        lengths = (cu[1:] - cu[:-1]).tolist()
+        assert cu[0] == 0 and cu[-1] == x.shape[0] and len(lengths) == conv.shape[0] == recurrent.shape[0]
+        want = [[i, j] for i, n in enumerate(lengths) for j in range(-(-n // 64))]
+        assert chunks.tolist() == want
+        pos = torch.cat([torch.arange(n, dtype=x.dtype) for n in lengths])
+        sums = torch.stack([p.sum() for p in x.split(lengths)])
+        calls.append(lengths)
+        out = x + pos.view(-1, 1)
+        result = (out, conv + sums.view(-1, 1, 1), recurrent + sums.view(-1, 1, 1, 1))
+        return result + (None,) if return_mixed else result
+
+    return run
+
+
+def test_eager_bookkeeping_follows_the_chunk_contract(serving):
+    """Eager prefills and extends of several requests through the host plan, with the packed pass replaced by
+    ``_transparent_packed``: after every call each new row's output is that row plus its position in the
+    pass that ran it (the committed pass takes the joined run of replayed tail + new rows up to its last 64-row
+    boundary as one sequence, the open pass the rest), the committed
+    states hold the sum of the request's rows up to its last 64-row boundary, the live states the sum of all
+    its rows, and the window its rows past that boundary (the brute-force statement of gdn.py:271-327)."""
+    hid = 8
+    batch = SimpleNamespace(is_decode=False, padded_size=0, gdn_prefill=None)
+    layer = serving.OriginalGDN(SimpleNamespace(hidden_size=hid), layer_id=1, batch_source=lambda: batch)
+    layer.allocate_cache(5, torch.device("cpu"), torch.float64)
+    calls = []
+    layer._run_packed = _transparent_packed(calls)
+    gen = torch.Generator().manual_seed(7)
+    history = {}  # slot -> all rows of its request so far
+    reqs = {}
+    schedule = [  # (slot, new rows) per call
+        [(0, 70), (1, 5), (2, 63), (4, 64)],
+        [(2, 1), (1, 59), (0, 130)],  # slot 2 completes its chunk exactly, slot 1 reaches 64 with its tail
+        [(3, 200), (1, 1), (2, 64), (0, 3)],
+        [(0, 58), (3, 56), (4, 1)],
+    ]
+    for step in schedule:
+        batch_reqs = []
+        for s, n in step:
+            r = reqs.setdefault(s, SimpleNamespace(table_idx=s, uid=10 + s, is_cfg_uncond=False, cached_len=0,
+                                                   device_len=0, extend_len=0))
+            r.cached_len, r.extend_len, r.device_len = r.device_len, n, r.device_len + n
+            batch_reqs.append(r)
+        batch.reqs = batch.padded_reqs = batch_reqs
+        x = torch.randn(sum(n for _, n in step), hid, generator=gen, dtype=torch.float64)
+        calls.clear()
+        y = layer.forward(x)
+        # the passes ran each request's unfinished tail and new rows once, nothing of its history before
+        assert sum(map(sum, calls)) == sum(len(history.get(s, [])) % 64 + n for s, n in step)
+        at = 0
+        for s, n in step:
+            old = history.get(s, x[:0])
+            cut = len(old) // 64 * 64  # the window before the call starts here
+            rows = torch.cat((old, x[at:at + n]))
+            for j in range(n):  # new row j sits at position len(old) + j of the request
+                p = len(old) + j
+                whole = cut + (len(rows) - cut) // 64 * 64  # the committed pass runs [cut, whole) as one run
+                base = cut if p < whole else whole
+                assert torch.equal(y[at + j], x[at + j] + (p - base)), (step, s, j)
+            history[s] = rows
+            at += n
+        for s, rows in history.items():
+            done = len(rows) // 64 * 64
+            assert torch.allclose(layer._conv_state[s], rows[:done].sum().expand(1536, 4)), s
+            assert torch.allclose(layer._recurrent_state[s], rows[:done].sum().expand(4, 128, 128).float()), s
+            assert torch.allclose(layer._live_conv[s], rows.sum().expand(1536, 4)), s
+            assert torch.allclose(layer._live_state[s], rows.sum().expand(4, 128, 128).float()), s
+            assert layer._win_len[s].item() == len(rows) - done and layer._lengths[s] == len(rows)
+            assert torch.equal(layer._window[s, : len(rows) - done], rows[done:]), s
+
+
+def test_plan_extend_splits_each_joined_run_at_its_last_chunk(serving):
+    """The host plan for three requests: a fresh one of 70 rows, one with a 10-row tail and 54 new rows (one
+    complete chunk, nothing open), one with a 3-row tail and 2 new rows (open only)."""
+    R = serving.Request
+    reqs = [R(slot=2, owner=(1, False), cached=0, new=70), R(slot=0, owner=(2, False), cached=74, new=54),
+            R(slot=3, owner=(3, False), cached=131, new=2)]
+    replayed, committed, open_ = serving.plan_extend(reqs)
+    assert replayed == list(range(0, 10)) + [3 * 64 + j for j in range(3)]
+    assert committed.members == [0, 1] and committed.lengths == [64, 64]
+    assert committed.src == [13 + j for j in range(64)] + list(range(10)) + [13 + 70 + j for j in range(54)]
+    assert committed.dest == list(range(64)) + list(range(70, 124))
+    assert committed.out_rows == list(range(64)) + list(range(74, 128))
+    assert open_.members == [0, 2] and open_.lengths == [6, 5]
+    assert open_.src == [13 + 64 + j for j in range(6)] + [10, 11, 12, 13 + 124, 13 + 125]
+    assert open_.dest == list(range(64, 70)) + [124, 125] and open_.out_rows == [0, 1, 2, 3, 4, 5, 9, 10]
+    assert open_.window == [2 * 64 + j for j in range(6)] + [3 * 64 + j for j in range(5)]
+    assert open_.member_of_row == [0] * 6 + [2] * 5

@@ -1,26 +1,32 @@
 """The serving layer's GDN mixer with request-local state, on the MI355X kernels.
 
-Mirrors ``OriginalGDN`` (``servers/sgl/src/zonos3_sgl/models/gdn.py:115-450``): the per-slot caches
-(``allocate_cache``, gdn.py:150-160), the ragged eager path (``forward``, gdn.py:235-327), the static-shape
-decode and prefill paths that CUDA/HIP graphs capture (gdn.py:329-393), the engine hooks (gdn.py:163-233)
-and ``_run_packed`` (gdn.py:395-450) through the five operator attributes, which are bound to this
-package's kernels (``fla_ops``).
+A drop-in for ``OriginalGDN`` (``servers/sgl/src/zonos3_sgl/models/gdn.py:115-450``): the same class,
+method and attribute names, the per-slot caches of ``allocate_cache`` (gdn.py:150-160), the engine hooks
+(gdn.py:163-233), the static-shape decode and prefill entries that graphs capture (gdn.py:329-393), the
+eager ragged forward (gdn.py:235-327) and ``_run_packed`` (gdn.py:395-450) through the five operator
+attributes, which are bound to this package's kernels (``fla_ops``).
 
-Exactness model (the reference's, kept): committed per-slot states end at a multiple of 64 rows of the
-request, and an eager forward replays the unfinished chunk (the tail, kept raw in a per-slot 64-row window)
-in front of the new rows, so prefill/extend cuts never change the chunk boundaries.
+Exactness model (the serving contract, kept): a slot's committed states end at a multiple of 64 rows of its
+request, and the request's unfinished chunk is kept raw in the slot's 64-row window, so a later call
+replays it in front of its new rows and prefill/extend/decode cuts never move a chunk boundary.
 
-The decode fast path. The reference's static decode recomputes each request's whole 64-row window through
-the chunk kernels on every step (gdn.py:329-355). Here every slot also keeps its *live* states, the conv
-history and the recurrent state after the request's last row, and a decode step (static or eager) is one
-single-row pass from them: ``in_proj`` on the new rows, one serving decode launch (conv/SiLU/L2/gate/delta
-rule/gated norm on the slots' caches in place, q/k rounded like the serving operators return them), ``wo``.
-The same launch writes the raw row into the slot's window and, when the window fills up, the new live states
-to the committed ones, so the eager path's tail replay stays what it was. Window rows past the fill are
-unspecified (only the eager replay reads windows, and only their filled rows). Live states are
-set by every path: the eager passes' final states (the uncommitted tail pass included: it has exact
-lengths), and the static prefill's window pass, whose zero padding rows are made exact no-ops of the state
-(decay 1, beta 0) so its final state is the state after the real rows.
+Design of this module.
+- Eager calls are planned on the host first (``plan_extend``): every request's replayed window rows and
+  new rows form one joined run, cut after its last complete chunk; the complete part goes to a committed
+  pass, the rest to an open pass. The plan is a set of index lists (source rows, output rows, window rows)
+  uploaded in one pinned copy; the device work is then one gather per pass, the packed pass itself and one
+  scatter of the outputs, whatever the number of requests.
+- ``_pass`` is the one place a packed pass touches the caches: it runs ``_run_packed`` from the slots'
+  committed states and stores the final states as live (and as committed for a committed pass). The eager
+  and static prefill paths both use it.
+- Decode never replays a window. Every slot also keeps *live* states (conv history and recurrent state
+  after the request's last row); a decode step (static or eager) is ``in_proj``, one serving decode launch
+  (conv/SiLU/L2/gate/delta rule/gated norm on the slots' caches in place, q/k rounded like the serving
+  operators return them) and ``wo``. The launch appends the raw row to the slot's window and, when the
+  window fills up, copies the live states to the committed ones.
+- Window rows past a slot's fill are unspecified: only the eager replay reads windows, and only their
+  filled rows. Padding rows of a static prefill window are made exact no-ops of the state (decay 1,
+  beta 0), so that pass's final state is the live state after the real rows.
 
 Engine integration: ``batch_source`` is a zero-argument callable returning the current batch (in the
 reference, ``get_global_ctx().batch``, gdn.py:236); ``accent`` optionally supplies the accent adapters'
@@ -32,7 +38,8 @@ are read by the reference's attribute names: ``is_decode``, ``padded_size``, ``g
 from __future__ import annotations
 
 import importlib
-from dataclasses import dataclass
+import itertools
+from dataclasses import dataclass, field
 from typing import Callable, Optional
 
 import torch
@@ -59,24 +66,31 @@ def device_tensor(values, dtype: torch.dtype, device) -> torch.Tensor:
     return host.pin_memory().to(device, non_blocking=True)
 
 
+def upload(lists: list[list[int]], dtype: torch.dtype, device) -> list[torch.Tensor]:
+    """Several host lists as contiguous 1-D ``device`` tensors, all in one transfer."""
+    flat = device_tensor([v for values in lists for v in values], dtype, device)
+    return list(flat.split([len(values) for values in lists]))
+
+
+def _table_lists(lengths: list[int]) -> tuple[list[int], list[int]]:
+    """cu_seqlens of packed sequences of ``lengths`` rows and their flattened (sequence, chunk) rows."""
+    cu = list(itertools.accumulate(lengths, initial=0))
+    pairs = [v for i, n in enumerate(lengths) for j in range(-(-n // CHUNK)) for v in (i, j)]
+    return cu, pairs
+
+
 def chunk_tables(lengths: list[int], device) -> tuple[torch.Tensor, torch.Tensor]:
     """(cu_seqlens int32 [n + 1], chunk indices int32 [chunks, 2] = (sequence, chunk within it)) of packed
-    sequences of ``lengths`` rows, in one non-blocking copy (gdn.py:49-59)."""
-    cu = [0]
-    pairs: list[int] = []
-    for i, n in enumerate(lengths):
-        cu.append(cu[-1] + n)
-        for j in range(-(-n // CHUNK)):
-            pairs += (i, j)
-    packed = device_tensor(cu + pairs, torch.int32, device)
-    return packed[: len(cu)], packed[len(cu):].view(-1, 2)
+    sequences of ``lengths`` rows, in one non-blocking copy (the tables of gdn.py:49-59)."""
+    cu, pairs = upload(list(_table_lists(lengths)), torch.int32, device)
+    return cu, pairs.view(-1, 2)
 
 
 @dataclass(frozen=True)
 class PrefillLayout:
-    """Static tables of a padded prefill (gdn.py:62-104): request i owns ``CHUNK * (whole[i] + 1)`` batch
-    rows from its start, its ``whole[i]`` complete chunks, then a 64-row window for its last ``n_i % 64``
-    rows (zeros after them)."""
+    """Static tables of a padded prefill (the engine builds one per tuple of complete-chunk counts,
+    gdn.py:62-104): request i owns ``CHUNK * (whole[i] + 1)`` consecutive batch rows, its ``whole[i]``
+    complete chunks and then a 64-row window that holds its last ``n_i % 64`` rows."""
 
     whole_rows: Optional[torch.Tensor]  # [sum 64 * whole] long: batch rows of the complete chunks
     whole_reqs: Optional[torch.Tensor]  # [k] long: batch index of each request with complete chunks
@@ -89,27 +103,28 @@ class PrefillLayout:
 
     @classmethod
     def build(cls, whole: list[int], device) -> "PrefillLayout":
-        starts, at = [], 0
-        for w in whole:
-            starts.append(at)
-            at += CHUNK * (w + 1)
-        with_whole = [i for i, w in enumerate(whole) if w]
-        whole_rows = [r for i in with_whole for r in range(starts[i], starts[i] + CHUNK * whole[i])]
-        window_rows = [r for i, w in enumerate(whole)
-                       for r in range(starts[i] + CHUNK * w, starts[i] + CHUNK * (w + 1))]
-        whole_cu = whole_chunks = None
-        if with_whole:
-            whole_cu, whole_chunks = chunk_tables([CHUNK * whole[i] for i in with_whole], device)
-        window_cu, window_chunks = chunk_tables([CHUNK] * len(whole), device)
+        """All tables from ``whole`` in two transfers (the int64 row tables, the int32 chunk tables)."""
+        owned = [CHUNK * w for w in whole]  # complete-chunk rows of each request
+        cut = list(itertools.accumulate((n + CHUNK for n in owned), initial=0))  # row after request i - 1
+        window_at = [c + n for c, n in zip(cut, owned)]  # first window row of each request
+        with_whole = [i for i, n in enumerate(owned) if n]
+        rows = upload([list(itertools.chain.from_iterable(range(cut[i], window_at[i]) for i in with_whole)),
+                       with_whole,
+                       [r for w in window_at for r in range(w, w + CHUNK)],
+                       owned], torch.long, device)
+        whole_cu, whole_pairs = _table_lists([owned[i] for i in with_whole])
+        window_cu, window_pairs = _table_lists([CHUNK] * len(whole))
+        tables = upload([whole_cu, whole_pairs, window_cu, window_pairs], torch.int32, device)
+        has_whole = bool(with_whole)
         return cls(
-            whole_rows=device_tensor(whole_rows, torch.long, device) if with_whole else None,
-            whole_reqs=device_tensor(with_whole, torch.long, device) if with_whole else None,
-            whole_cu=whole_cu,
-            whole_chunks=whole_chunks,
-            window_rows=device_tensor(window_rows, torch.long, device),
-            window_base=device_tensor([CHUNK * w for w in whole], torch.long, device),
-            window_cu=window_cu,
-            window_chunks=window_chunks,
+            whole_rows=rows[0] if has_whole else None,
+            whole_reqs=rows[1] if has_whole else None,
+            whole_cu=tables[0] if has_whole else None,
+            whole_chunks=tables[1].view(-1, 2) if has_whole else None,
+            window_rows=rows[2],
+            window_base=rows[3],
+            window_cu=tables[2],
+            window_chunks=tables[3].view(-1, 2),
         )
 
     def tensors(self) -> list[torch.Tensor]:
@@ -124,6 +139,72 @@ class PrefillInputs:
     layout: PrefillLayout
     slots: torch.Tensor  # [b] long: the requests' table slots
     lengths: torch.Tensor  # [b] long: the requests' real rows
+
+
+# --------------------------------------------------------------------------------- eager-call planning
+
+@dataclass(frozen=True)
+class Request:
+    """One request of an eager call as the mixer uses it (read from the engine's request object)."""
+
+    slot: int
+    owner: tuple  # (uid, is_cfg_uncond)
+    cached: int  # rows the slot already holds (committed states + window fill)
+    new: int  # rows in this call
+
+    @property
+    def replay(self) -> int:
+        """Rows of the unfinished chunk, replayed from the slot's window in front of the new rows."""
+        return self.cached % CHUNK
+
+    @property
+    def end(self) -> int:
+        return self.cached + self.new
+
+
+@dataclass
+class PackedPass:
+    """One packed pass of an eager call as host index lists. Source rows index the call's source: the
+    replayed window rows of all requests in request order, then the call's rows ``x``."""
+
+    commit: bool  # complete chunks (states committed) or the open remainders (live states only)
+    members: list[int] = field(default_factory=list)  # request index of each packed sequence
+    lengths: list[int] = field(default_factory=list)  # rows of each packed sequence
+    src: list[int] = field(default_factory=list)  # source row of each pass row
+    member_of_row: list[int] = field(default_factory=list)  # member request of each pass row
+    out_rows: list[int] = field(default_factory=list)  # pass rows that are new rows of the call ...
+    dest: list[int] = field(default_factory=list)  # ... and their rows in x (and in the result)
+    window: list[int] = field(default_factory=list)  # open pass: flat window row (slot * 64 + j) of each row
+
+
+def plan_extend(reqs: list[Request]) -> tuple[list[int], PackedPass, PackedPass]:
+    """(flat window rows to replay, the committed pass, the open pass) of an eager call. Request i's joined
+    run is its ``replay`` window rows then its ``new`` rows; its first ``joined // 64 * 64`` rows go to the
+    committed pass and the rest to the open pass, whose rows become the slot's new window."""
+    replayed = [r.slot * CHUNK + j for r in reqs for j in range(r.replay)]
+    first_new = len(replayed)
+    committed, open_ = PackedPass(commit=True), PackedPass(commit=False)
+    at_replay = at_new = 0
+    for i, r in enumerate(reqs):
+        joined = list(range(at_replay, at_replay + r.replay)) + list(range(first_new + at_new,
+                                                                           first_new + at_new + r.new))
+        cut = len(joined) - len(joined) % CHUNK
+        for part, lo, hi in ((committed, 0, cut), (open_, cut, len(joined))):
+            if hi == lo:
+                continue
+            part.members.append(i)
+            part.lengths.append(hi - lo)
+            for p in range(lo, hi):
+                if p >= r.replay:
+                    part.out_rows.append(len(part.src))
+                    part.dest.append(at_new + p - r.replay)
+                if not part.commit:
+                    part.window.append(r.slot * CHUNK + p - lo)
+                part.src.append(joined[p])
+                part.member_of_row.append(i)
+        at_replay += r.replay
+        at_new += r.new
+    return replayed, committed, open_
 
 
 class _Weight:
@@ -169,24 +250,28 @@ class OriginalGDN:
         self._lengths = [0] * capacity
         self._capacity = capacity
 
+    def _reset_slots(self, idx: torch.Tensor) -> None:
+        for t in (self._conv_state, self._recurrent_state, self._live_conv, self._live_state, self._window,
+                  self._win_len):
+            t.index_fill_(0, idx, 0)
+
     # ----------------------------------------------------------------------------------- engine hooks
 
     @staticmethod
     def static_tables(device, bs_list) -> dict[int, tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
-        """Per batch size: (cu_seqlens of bs 64-row windows, their chunk indices, row offsets bs * 64)
-        (gdn.py:163-172). The fast decode path reads only the row offsets."""
-        tables = {}
-        for bs in bs_list:
+        """Per batch size bs: the chunk tables of bs 64-row windows and each window's first row
+        (the contract of gdn.py:163-172). The fast decode path reads only the first rows."""
+        def windows(bs):
             cu, chunks = chunk_tables([CHUNK] * bs, device)
-            tables[bs] = (cu, chunks, torch.arange(bs, device=device, dtype=torch.long) * CHUNK)
-        return tables
+            return cu, chunks, cu[:-1].to(torch.long)
+
+        return {bs: windows(bs) for bs in bs_list}
 
     def enable_graph_decode(self, slots: torch.Tensor, tables) -> None:
         """``slots``: the engine's static [max_bs] int64 buffer of table slots of the padded decode batch,
         filled before every capture / replay; ``tables`` from ``static_tables`` (gdn.py:174-183)."""
         self._graph_slots = slots
-        for bs, (_, _, rows) in tables.items():
-            self._static_rows[bs] = rows
+        self._static_rows.update({bs: entry[2] for bs, entry in tables.items()})
 
     @staticmethod
     def pin_fla_cache(static_tensors, pinned: dict) -> int:
@@ -215,8 +300,8 @@ class OriginalGDN:
         return None if self._accent is None else self._accent.accent_mask()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """gdn.py:235-327: static decode / static prefill when the batch asks for them, else the ragged
-        eager path over the batch's requests (validated before any cache changes)."""
+        """Static decode / static prefill when the batch asks for them, else the eager path over the
+        batch's requests, which checks the whole batch before it changes any cache (gdn.py:235-327)."""
         batch = self._current_batch()
         if batch.is_decode and self._static_mode:
             return self._forward_decode_static(x, batch.padded_size)
@@ -224,90 +309,97 @@ class OriginalGDN:
             return self._forward_prefill_static(x, batch.gdn_prefill)
         if x.is_cuda and torch.cuda.is_current_stream_capturing():
             raise RuntimeError("GDN ragged path cannot be captured; graphs use the static window / prefill paths")
-        reqs = batch.reqs
-        if len(batch.padded_reqs) != len(reqs):
-            raise RuntimeError("GDN eager path does not accept dummy graph-padding requests")
-        slots = [r.table_idx for r in reqs]
-        lengths = [r.extend_len for r in reqs]
-        if (not self._capacity or len(set(slots)) != len(slots)
-                or any(s < 0 or s >= self._capacity for s in slots)
-                or any(n <= 0 for n in lengths) or sum(lengths) != x.shape[0]):
-            raise RuntimeError("Invalid GDN request slots or packed lengths")
-        if batch.is_decode and any(n != 1 for n in lengths):
-            raise RuntimeError("GDN decode expects one new token per request")
-        owners = [(r.uid, r.is_cfg_uncond) for r in reqs]
-        for r, owner in zip(reqs, owners):  # a KV-only prefix hit has no recurrent state: rejected
-            s = r.table_idx
-            if r.cached_len and (self._owners[s] != owner or self._lengths[s] != r.cached_len):
-                raise RuntimeError(
-                    f"GDN layer {self._layer_id}: missing/stale state at slot {s}; "
-                    f"expected {(owner, r.cached_len)}, found {(self._owners[s], self._lengths[s])}")
+        reqs = self._admit(batch, x.shape[0])
         mask = self._accent_mask()
-        if mask is not None:  # one [K] row per request: its first new row's
-            starts = [sum(lengths[:i]) for i in range(len(lengths))]
-            mask = mask.index_select(0, device_tensor(starts, torch.long, mask.device))
-        fresh = [r.table_idx for r in reqs if r.cached_len == 0]
+        if mask is not None:  # a request's adapters: the mask row of its first new row
+            firsts = list(itertools.accumulate((r.new for r in reqs[:-1]), initial=0))
+            mask = mask.index_select(0, device_tensor(firsts, torch.long, mask.device))
+        fresh = [r.slot for r in reqs if r.cached == 0]
         if fresh:
             self._reset_slots(device_tensor(fresh, torch.long, x.device))
         if batch.is_decode:
-            y = self._decode_rows(x, device_tensor(slots, torch.long, x.device), mask)
+            y = self._decode_rows(x, device_tensor([r.slot for r in reqs], torch.long, x.device), mask)
         else:
-            y = self._extend(x, reqs, slots, lengths, mask)
-        for r, owner in zip(reqs, owners):
-            self._owners[r.table_idx] = owner
-            self._lengths[r.table_idx] = r.device_len
+            y = self._extend(x, reqs, mask)
+        for r in reqs:
+            self._owners[r.slot] = r.owner
+            self._lengths[r.slot] = r.end
         return y
 
-    def _reset_slots(self, idx: torch.Tensor) -> None:
-        for t in (self._conv_state, self._recurrent_state, self._live_conv, self._live_state, self._window,
-                  self._win_len):
-            t.index_fill_(0, idx, 0)
+    def _admit(self, batch, rows: int) -> list[Request]:
+        """The eager batch's requests after every check (a failed check raises RuntimeError before any
+        cache changes). A request that continues a slot must find the slot holding exactly its rows: a
+        prefix matched in the KV cache alone has no recurrent state here and is refused."""
+        where = f"GDN layer {self._layer_id} eager call"
+        if not self._capacity:
+            raise RuntimeError(f"{where}: allocate_cache was not called")
+        if len(batch.padded_reqs) != len(batch.reqs):
+            raise RuntimeError(f"{where}: {len(batch.padded_reqs) - len(batch.reqs)} dummy graph-padding "
+                               f"requests (only the static paths take them)")
+        reqs, taken = [], set()
+        for r in batch.reqs:
+            s, n = r.table_idx, r.extend_len
+            if not 0 <= s < self._capacity:
+                raise RuntimeError(f"{where}: slot {s} outside the {self._capacity} slots of the cache")
+            if s in taken:
+                raise RuntimeError(f"{where}: slot {s} named by two requests")
+            taken.add(s)
+            if n <= 0:
+                raise RuntimeError(f"{where}: the request in slot {s} brings {n} rows")
+            if batch.is_decode and n != 1:
+                raise RuntimeError(f"{where}: a decode batch takes one new row per request, slot {s} has {n}")
+            owner = (r.uid, r.is_cfg_uncond)
+            if r.cached_len and (self._owners[s] != owner or self._lengths[s] != r.cached_len):
+                raise RuntimeError(f"{where}: slot {s} has no state for {owner} at row {r.cached_len} "
+                                   f"(it holds {self._owners[s]} at row {self._lengths[s]})")
+            reqs.append(Request(slot=s, owner=owner, cached=r.cached_len, new=n))
+        if sum(r.new for r in reqs) != rows:
+            raise RuntimeError(f"{where}: {rows} rows given for requests of {sum(r.new for r in reqs)} rows")
+        return reqs
 
-    def _extend(self, x, reqs, slots, lengths, mask):
-        """The eager prefill / extend (gdn.py:271-327): replay each request's tail in front of its new rows;
-        complete chunks in a committed pass, the rest in an uncommitted pass whose final states are the
-        live ones."""
-        pieces = x.split(lengths)
-        combined, old_tail, complete = [], [], []
-        for r, new in zip(reqs, pieces):
-            tail = self._window[r.table_idx, : r.cached_len % CHUNK] if r.cached_len else new[:0]
-            old_tail.append(len(tail))
-            joined = torch.cat((tail, new)) if len(tail) else new
-            combined.append(joined)
-            complete.append(len(joined) // CHUNK * CHUNK)
-        outputs: list[list[torch.Tensor]] = [[] for _ in reqs]
+    def _pass(self, rows, cu, chunks, slots, commit: bool, mask=None, valid=None, live_conv=True):
+        """``_run_packed`` over packed sequences from the committed states of ``slots``; the final states
+        become the slots' live states and, for a committed pass, their committed states. Returns the
+        output rows and the projection rows (``mixed``)."""
+        out, conv_final, final, mixed = self._run_packed(
+            rows, cu, chunks, self._conv_state.index_select(0, slots), self._recurrent_state.index_select(0, slots),
+            mask, valid=valid, return_mixed=True)
+        final = final.float()
+        if commit:
+            self._conv_state.index_copy_(0, slots, conv_final)
+            self._recurrent_state.index_copy_(0, slots, final)
+        if live_conv:
+            self._live_conv.index_copy_(0, slots, conv_final)
+        self._live_state.index_copy_(0, slots, final)
+        return out, mixed
 
-        def run(which, values, commit):
-            idx = device_tensor([slots[i] for i in which], torch.long, x.device)
-            rows = None if mask is None else torch.cat([mask[i].expand(len(v), -1) for i, v in zip(which, values)])
-            cu, chunks = chunk_tables([len(v) for v in values], x.device)
-            out, conv_final, final = self._run_packed(
-                torch.cat(values), cu, chunks, self._conv_state.index_select(0, idx),
-                self._recurrent_state.index_select(0, idx), rows)
-            for i, y in zip(which, out.split([len(v) for v in values])):
-                outputs[i].append(y)
-            final = final.float()
-            if commit:
-                self._conv_state.index_copy_(0, idx, conv_final)
-                self._recurrent_state.index_copy_(0, idx, final)
-            self._live_conv.index_copy_(0, idx, conv_final)
-            self._live_state.index_copy_(0, idx, final)
-
-        whole = [i for i, n in enumerate(complete) if n]
-        if whole:
-            run(whole, [combined[i][: complete[i]] for i in whole], True)
-        partial = [i for i, v in enumerate(combined) if complete[i] < len(v)]
-        if partial:
-            run(partial, [combined[i][complete[i]:] for i in partial], False)
-        tails = []
-        for i, r in enumerate(reqs):
-            tail = combined[i][complete[i]:]
-            self._window[r.table_idx, : len(tail)] = tail
-            self._window[r.table_idx, len(tail):].zero_()
-            tails.append(len(tail))
-        self._win_len.index_copy_(0, device_tensor(slots, torch.long, x.device),
-                                  device_tensor(tails, torch.int32, x.device))
-        return torch.cat([torch.cat(parts)[n:] for parts, n in zip(outputs, old_tail)])
+    def _extend(self, x, reqs: list[Request], mask):
+        """An eager prefill / extend (gdn.py:271-327) by the host plan: the committed pass, then the open
+        pass (from the states the committed pass left), then the new windows."""
+        replayed, *passes = plan_extend(reqs)
+        passes = [p for p in passes if p.members]
+        dev, hid = x.device, self._hidden
+        idx = iter(upload([replayed] + [lst for p in passes for lst in (
+            p.src, p.member_of_row, p.out_rows, p.dest, p.window, [reqs[i].slot for i in p.members])]
+            + [[r.slot for r in reqs], [r.end % CHUNK for r in reqs]], torch.long, dev))
+        tables = iter(upload([lst for p in passes for lst in _table_lists(p.lengths)], torch.int32, dev))
+        src = x
+        replay_idx = next(idx)
+        if replayed:  # gathered before any window is rewritten
+            src = torch.cat((self._window.view(-1, hid).index_select(0, replay_idx), x))
+        y = torch.empty_like(x)
+        for p in passes:
+            src_idx, member_of_row, out_rows, dest, window, slots = (next(idx) for _ in range(6))
+            cu, pairs = next(tables), next(tables)
+            rows = src.index_select(0, src_idx)
+            out, _ = self._pass(rows, cu, pairs.view(-1, 2), slots, p.commit,
+                                mask=None if mask is None else mask.index_select(0, member_of_row))
+            y.index_copy_(0, dest, out if len(p.out_rows) == len(p.src) else out.index_select(0, out_rows))
+            if not p.commit:
+                self._window.view(-1, hid).index_copy_(0, window, rows)
+        all_slots, fill = next(idx), next(idx)
+        self._win_len.index_copy_(0, all_slots, fill.to(torch.int32))
+        return y
 
     def _forward_decode_static(self, x: torch.Tensor, bs: int) -> torch.Tensor:
         """One new row per padded request (gdn.py:329-355); every shape depends on ``bs`` only, so the step
@@ -335,10 +427,12 @@ class OriginalGDN:
             y = self._accent.apply_accent(self.wo, out, y, mask)
         return y
 
+
     def _forward_prefill_static(self, x: torch.Tensor, inputs: PrefillInputs) -> torch.Tensor:
-        """A padded prefill of fresh requests (gdn.py:357-393): the committed pass over the complete chunks,
-        then each request's last ``n % 64`` rows as a 64-row window with zeros after them. The window's
-        padding rows get decay 1 and beta 0, so its final states are the live ones."""
+        """A padded prefill of fresh requests on the layout's fixed shapes (the contract of gdn.py:357-393):
+        a committed pass over the complete chunks, then an open pass over every request's 64-row window, in
+        which the rows past the request's real rows are zeroed and made state no-ops. The final states of
+        the open pass are the live ones; the windows keep the rows."""
         if self._accent_mask() is not None:
             raise RuntimeError("GDN static prefill does not take accent adapters")
         layout, slots = inputs.layout, inputs.slots
@@ -346,30 +440,24 @@ class OriginalGDN:
         self._reset_slots(slots)
         y = torch.empty_like(x)
         if layout.whole_rows is not None:
-            whole_slots = slots.index_select(0, layout.whole_reqs)
-            out, conv_final, final = self._run_packed(
-                x.index_select(0, layout.whole_rows), layout.whole_cu, layout.whole_chunks,
-                self._conv_state.index_select(0, whole_slots), self._recurrent_state.index_select(0, whole_slots))
-            self._conv_state.index_copy_(0, whole_slots, conv_final)
-            self._recurrent_state.index_copy_(0, whole_slots, final.float())
+            out, _ = self._pass(x.index_select(0, layout.whole_rows), layout.whole_cu, layout.whole_chunks,
+                                slots.index_select(0, layout.whole_reqs), commit=True)
             y.index_copy_(0, layout.whole_rows, out)
-        tail = inputs.lengths - layout.window_base  # real rows in each window
-        real = torch.arange(CHUNK, device=x.device).view(1, CHUNK) < tail.view(bs, 1)
-        win = x.index_select(0, layout.window_rows).masked_fill(~real.view(-1, 1), 0)
-        conv0 = self._conv_state.index_select(0, slots)
-        out, _, final, mixed = self._run_packed(win, layout.window_cu, layout.window_chunks, conv0,
-                                                self._recurrent_state.index_select(0, slots),
-                                                valid=real.view(-1), return_mixed=True)
+        fill = (inputs.lengths - layout.window_base).to(torch.int32)  # real rows of each window
+        # a padding row is a state no-op only if its values are finite (beta 0 multiplies them): zero them
+        real = torch.arange(CHUNK, device=x.device, dtype=torch.int32).unsqueeze(0) < fill.unsqueeze(1)
+        win = torch.where(real.view(-1, 1), x.index_select(0, layout.window_rows), x.new_zeros(()))
+        out, mixed = self._pass(win, layout.window_cu, layout.window_chunks, slots, commit=False,
+                                valid=real.view(-1), live_conv=False)
         y.index_copy_(0, layout.window_rows, out)
-        # live conv: the last four raw inputs before the window's padding (committed history first)
+        # live conv history: the last CONV_WIDTH conv inputs up to each window's last real row, the
+        # committed history (zero for fresh requests, or the complete chunks' end) standing before row 0
         raw = mixed[:, :CONV_CHANNELS].reshape(bs, CHUNK, CONV_CHANNELS).transpose(1, 2)
-        hist = torch.cat((conv0, raw), dim=-1)  # [bs, C, 4 + 64]
-        pick = (tail.view(bs, 1, 1) + torch.arange(CONV_WIDTH, device=x.device).view(1, 1, -1)).expand(
-            bs, CONV_CHANNELS, CONV_WIDTH)
-        self._live_conv.index_copy_(0, slots, torch.gather(hist, 2, pick))
-        self._live_state.index_copy_(0, slots, final.float())
+        hist = torch.cat((self._conv_state.index_select(0, slots), raw), dim=-1)  # [bs, C, CONV_WIDTH + 64]
+        take = fill.to(torch.long).view(bs, 1, 1) + torch.arange(CONV_WIDTH, device=x.device).view(1, 1, -1)
+        self._live_conv.index_copy_(0, slots, hist.gather(2, take.expand(bs, CONV_CHANNELS, CONV_WIDTH)))
         self._window.index_copy_(0, slots, win.view(bs, CHUNK, self._hidden))
-        self._win_len.index_copy_(0, slots, tail.to(torch.int32))
+        self._win_len.index_copy_(0, slots, fill)
         return y
 
     def _run_packed(self, x, cu, chunks, conv, recurrent, mask=None, valid=None, return_mixed=False):
