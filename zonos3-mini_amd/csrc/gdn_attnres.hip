@@ -70,6 +70,21 @@ __device__ __forceinline__ void round2_t(float& a, float& b) {
   }
 }
 
+// a.lo * b.lo + a.hi * b.hi + c for two bf16 pairs (v_dot2c_f32_bf16): the products of bf16 values are exact
+// in fp32, so with one half of b zero this is an exact product (plus c), and with b = (1, 1) the fp32 sum of
+// the two halves of a (plus c).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+constexpr uint32_t BF16_ONE_HI = 0x3f800000u, BF16_ONES = 0x3f803f80u;
+// (1, 0): bf16 1.0 in the low half, in a register. As an immediate, the compiler encodes this operand as the
+// inline constant 1.0, which the instruction reads as the fp32 word 0x3f800000, i.e. (0, 1).
+__device__ __forceinline__ uint32_t bf16_one_lo() {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, 0x3f80" : "=v"(r));
+  return r;
+}
+
 // NCH: 8-element pieces per lane (dim <= 512 NCH); columns past dim are masked.
 template <typename T, int NCH>
 __global__ __launch_bounds__(64 * AR_WAVES) void attnres_kernel(const SourcePtrs src, int n_sources, int dim,
@@ -78,7 +93,7 @@ __global__ __launch_bounds__(64 * AR_WAVES) void attnres_kernel(const SourcePtrs
   __shared__ float s_acc[AR_WAVES][NCH * 8][64];
   __shared__ float s_logit[AR_MAX_SOURCES];
   const int token = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   bool on[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) on[c] = 8 * (lane + 64 * c) < dim;
@@ -162,11 +177,11 @@ __global__ __launch_bounds__(64 * AR_WAVES) void attnres_kernel(const SourcePtrs
   }
 }
 
-// The register-resident form (the release LM's bank: dim 1024, up to 64 sources): AR_RWAVES waves per token,
-// wave w owns sources w + AR_RWAVES j (j < R) and issues all their loads at once, keeping the raw rows in
-// registers for both passes (each row read from memory once, no second read). Same arithmetic as above.
-constexpr int AR_RWAVES = 8;
-
+// The register-resident form (the release LM's bank: dim 1024, up to 64 sources): a workgroup of W waves per
+// token (4 for a bf16 bank, 8 for fp32); wave w owns the sources w + W j (j < R), issues all their loads at
+// once and holds the raw rows in registers for both passes (each row read from memory once). (A persistent
+// form that loaded the next token's rows into a second register set while mixing the current one measured
+// slower: the second set halves the resident workgroups.)
 template <typename T>
 struct raw8;  // 8 consecutive elements as loaded
 template <>
@@ -196,141 +211,213 @@ struct raw8<float> {
 };
 
 template <typename T, int NCH, int R>
-__global__ __launch_bounds__(64 * AR_RWAVES) void attnres_reg_kernel(const SourcePtrs src, int n_sources, int dim,
-                                                                       long row_stride, const T* __restrict__ query,
-                                                                       float eps, T* __restrict__ out) {
-  __shared__ float s_acc[AR_RWAVES / 2][NCH * 8][64];
-  __shared__ float s_logit[AR_MAX_SOURCES];
-  const int token = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct RowSet {
+  typename raw8<T>::type x[R][NCH];
+};
+
+// The query as the passes use it: for bf16, each pair word split into (q_2i, 0) and (0, q_2i+1) words; for fp32
+// the values.
+template <typename T, int NCH>
+struct QueryRegs {
+  uint32_t lo[NCH][4], hi[NCH][4];
+  float f[NCH][8];
+};
+
+// Every owned row of one token: the row pointers first (scalar loads, all in flight together), then the rows,
+// unconditionally (a wave's slots past the last source re-read the last source's row and columns past dim
+// re-read the row's last 8 columns; both are ignored), so that the compiler's wait counts stay exact.
+template <typename T, int NCH, int R, int W>
+__device__ __forceinline__ RowSet<T, NCH, R> load_rowset(const SourcePtrs& src, int n_sources, int dim,
+                                                         long row_stride, int token, int wave, int lane) {
+  RowSet<T, NCH, R> rs;
+  const T* rows[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    rows[j] = reinterpret_cast<const T*>(src.p[min(wave + W * j, n_sources - 1)]) + (size_t)token * row_stride;
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) rs.x[j][c] = raw8<T>::load(rows[j] + min(8 * (lane + 64 * c), dim - 8));
+  return rs;
+}
+
+template <typename T, int NCH, int R, int W>
+struct MixSm {
+  // the waves' partial mixes, element (c, i) of lane l at [wave][8 c + i][l] (rows padded to 72 floats so that
+  // the final sums' reads, 4 lanes x 4 element pairs, fall on 64 different banks)
+  float acc[W][NCH * 8][72];
+  float logit[AR_MAX_SOURCES];
+};
+
+// One token's mix from its rows in registers. Two workgroup barriers: after the logits (before the softmax
+// reads them) and after the partial mixes (before the final sums read them).
+template <typename T, int NCH, int R, int W>
+__device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const QueryRegs<T, NCH> qr,
+                                          MixSm<T, NCH, R, W>& sm, int n_sources, int dim, float eps, int token,
+                                          int wave, int lane, T* __restrict__ out) {
   bool on[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) on[c] = 8 * (lane + 64 * c) < dim;
-  // every owned row's loads first (a source past n_sources or a column past dim is not read)
-  typename raw8<T>::type xr[R][NCH];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const int s = wave + AR_RWAVES * j;
-    const T* row = reinterpret_cast<const T*>(src.p[min(s, n_sources - 1)]) + (size_t)token * row_stride;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      if (s < n_sources && on[c]) xr[j][c] = raw8<T>::load(row + 8 * (lane + 64 * c));
-  }
-  float q[NCH][8];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    if (on[c]) row8<T>::load(query + 8 * (lane + 64 * c), q[c]);
-    else
-      for (int i = 0; i < 8; ++i) q[c][i] = 0.f;
-  }
   const float inv_dim = 1.f / (float)dim;
-  // pass 1: logits
+  // pass 1: logit_s = sum round(round(x r) q), r = rsqrt(mean(x^2) + eps)
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const int s = wave + AR_RWAVES * j;
+    const int s = wave + W * j;
     if (s >= n_sources) break;
-    float x[NCH][8], ss = 0.f;
+    float ss = 0.f, lg = 0.f;
+    if constexpr (sizeof(T) == 2) {
+      // bf16 bank: the same rounding points with the exact products and the fp32 sums on v_dot2c_f32_bf16
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (on[c]) raw8<T>::unpack(xr[j][c], x[c]);
-      else
-        for (int i = 0; i < 8; ++i) x[c][i] = 0.f;
+      for (int c = 0; c < NCH; ++c)
+        if (on[c]) {
+          const uint4 w = xr.x[j][c];
+          ss = dot2_bf16(w.x, w.x, dot2_bf16(w.y, w.y, dot2_bf16(w.z, w.z, dot2_bf16(w.w, w.w, ss))));
+        }
+      const float r = rsqrtf(wave_sum(ss) * inv_dim + eps);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(x[c][i], x[c][i], ss);
-    }
-    const float r = rsqrtf(wave_sum(ss) * inv_dim + eps);
-    float lg = 0.f;
+      for (int c = 0; c < NCH; ++c)
+        if (on[c]) {
+          const uint4 w = xr.x[j][c];
+          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t k = pack_bf16x2(__uint_as_float(u[i] << 16) * r, __uint_as_float(u[i] & 0xffff0000u) * r);
+            const uint32_t pq = pack_bf16x2(dot2_bf16(k, qr.lo[c][i], 0.f), dot2_bf16(k, qr.hi[c][i], 0.f));
+            lg = dot2_bf16(pq, BF16_ONES, lg);
+          }
+        }
+    } else {
+      float x[NCH][8];
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        float k0 = x[c][i] * r, k1 = x[c][i + 1] * r;
-        round2_t<T>(k0, k1);
-        float p0 = k0 * q[c][i], p1 = k1 * q[c][i + 1];
-        round2_t<T>(p0, p1);
-        lg += p0;
-        lg += p1;
+      for (int c = 0; c < NCH; ++c) {
+        raw8<T>::unpack(xr.x[j][c], x[c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (!on[c]) x[c][i] = 0.f;
+          ss = fmaf(x[c][i], x[c][i], ss);
+        }
       }
+      const float r = rsqrtf(wave_sum(ss) * inv_dim + eps);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lg += x[c][i] * r * qr.f[c][i];
+    }
     lg = wave_sum(lg);
-    if (lane == 0) s_logit[s] = lg;
+    if (lane == 0) sm.logit[s] = lg;
   }
   __syncthreads();
-  float mx = -INFINITY;
-  for (int s = 0; s < n_sources; ++s) mx = fmaxf(mx, s_logit[s]);
-  float den = 0.f;
-  for (int s = 0; s < n_sources; ++s) den += __expf(s_logit[s] - mx);
-  const float inv_den = 1.f / den;
-  // pass 2 from the registers
+  // softmax with one source per lane: e_s = exp(logit_s - max) in lane s, weight_s = e_s / sum e
+  // (the cross-lane reductions run with every lane active)
+  const float lg_l = lane < n_sources ? sm.logit[lane] : -INFINITY;
+  const float mx = wave_max(lg_l);
+  const float e_l = lane < n_sources ? __expf(lg_l - mx) : 0.f;
+  const float inv_den = 1.f / wave_sum(e_l);
+  // pass 2: sum_s round(w_s x_s) over this wave's sources
   float acc[NCH][8];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
+#pragma unroll
     for (int i = 0; i < 8; ++i) acc[c][i] = 0.f;
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const int s = wave + AR_RWAVES * j;
+    const int s = wave + W * j;
     if (s >= n_sources) break;
-    const float w = round_to_t<T>(__expf(s_logit[s] - mx) * inv_den);
+    const float w = round_to_t<T>(__shfl(e_l, s) * inv_den);
+    if constexpr (sizeof(T) == 2) {
+      // round(x w): exact products on (w, 0) / (0, w) words; the fp32 sums on (1, 0) / (0, 1) words
+      const uint32_t wl = __float_as_uint(w) >> 16, wh = __float_as_uint(w) & 0xffff0000u;
+      const uint32_t one_lo = bf16_one_lo();
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (!on[c]) continue;
-      float x[8];
-      raw8<T>::unpack(xr[j][c], x);
+      for (int c = 0; c < NCH; ++c) {
+        const uint4 xw = xr.x[j][c];
+        const uint32_t u[4] = {xw.x, xw.y, xw.z, xw.w};
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        float y0 = x[i] * w, y1 = x[i + 1] * w;
-        round2_t<T>(y0, y1);
-        acc[c][i] += y0;
-        acc[c][i + 1] += y1;
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t y = pack_bf16x2(dot2_bf16(u[i], wl, 0.f), dot2_bf16(u[i], wh, 0.f));
+          acc[c][2 * i] = dot2_bf16(y, one_lo, acc[c][2 * i]);
+          acc[c][2 * i + 1] = dot2_bf16(y, BF16_ONE_HI, acc[c][2 * i + 1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float x[8];
+        raw8<T>::unpack(xr.x[j][c], x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[c][i] += x[i] * w;
       }
     }
   }
-  // waves 4-7 hand their sums to waves 0-3, each of which adds its partner's; wave 0 adds the four results
-  if (wave >= AR_RWAVES / 2) {
+  // the waves' partial mixes through LDS; then every thread finishes two adjacent columns (a wave 128 of them)
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+  for (int c = 0; c < NCH; ++c)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) s_acc[wave - AR_RWAVES / 2][c * 8 + i][lane] = acc[c][i];
-  }
+    for (int i = 0; i < 8; ++i) sm.acc[wave][c * 8 + i][lane] = acc[c][i];
   __syncthreads();
-  if (wave < AR_RWAVES / 2) {
+  for (int pr = threadIdx.x; pr < NCH * 256; pr += 64 * W) {
+    const int col = 2 * pr, c = col >> 9, l = (col & 511) >> 3, i = col & 7;
+    if (col >= dim) break;
+    float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s_acc[wave][c * 8 + i][lane] += acc[c][i];
+    for (int w = 0; w < W; ++w) {
+      o0 += sm.acc[w][c * 8 + i][l];
+      o1 += sm.acc[w][c * 8 + i + 1][l];
+    }
+    if constexpr (sizeof(T) == 2)
+      *reinterpret_cast<uint32_t*>(out + (size_t)token * dim + col) = pack_bf16x2(o0, o1);
+    else
+      *reinterpret_cast<float2*>(out + (size_t)token * dim + col) = make_float2(o0, o1);
   }
-  __syncthreads();
-  if (wave == 0) {
+}
+
+template <typename T, int NCH, int R, int W>
+__global__ __launch_bounds__(64 * W) void attnres_reg_kernel(const SourcePtrs src, int n_sources, int tokens,
+                                                             int dim, long row_stride, const T* __restrict__ query,
+                                                             float eps, T* __restrict__ out) {
+  __shared__ MixSm<T, NCH, R, W> sm;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  QueryRegs<T, NCH> qr;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (!on[c]) continue;
-      float o[8];
+  for (int c = 0; c < NCH; ++c) {
+    const bool on = 8 * (lane + 64 * c) < dim;
+    if constexpr (sizeof(T) == 2) {
+      const uint4 w = on ? *reinterpret_cast<const uint4*>(query + 8 * (lane + 64 * c)) : make_uint4(0, 0, 0, 0);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v = 0.f;
-#pragma unroll
-        for (int w = 0; w < AR_RWAVES / 2; ++w) v += s_acc[w][c * 8 + i][lane];
-        o[i] = v;
+      for (int i = 0; i < 4; ++i) {
+        qr.lo[c][i] = u[i] & 0xffffu;
+        qr.hi[c][i] = u[i] & 0xffff0000u;
       }
-      row8<T>::store(out + (size_t)token * dim + 8 * (lane + 64 * c), o);
+    } else {
+      if (on) row8<T>::load(query + 8 * (lane + 64 * c), qr.f[c]);
+      else
+        for (int i = 0; i < 8; ++i) qr.f[c][i] = 0.f;
     }
   }
+  const int t = blockIdx.x;
+  mix_token<T, NCH, R, W>(load_rowset<T, NCH, R, W>(src, n_sources, dim, row_stride, t, wave, lane), qr, sm,
+                          n_sources, dim, eps, t, wave, lane, out);
 }
 
 template <typename T>
 void launch_attnres(const SourcePtrs& p, int n_sources, int tokens, int dim, long row_stride, const void* query,
                     float eps, void* out, hipStream_t stream) {
   const int nch = (dim + 511) / 512;
-  const int r = (n_sources + AR_RWAVES - 1) / AR_RWAVES;  // rows per wave of the register-resident form
-  const int rr = r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : 8;
+  constexpr int W = sizeof(T) == 2 ? 4 : 8;  // waves per token of the register-resident form
+  const int r = (n_sources + W - 1) / W;     // rows per wave
+  const int rr = r <= 4 ? r : r <= 6 ? 6 : 8;
   if (nch <= 2 && nch * rr * (int)sizeof(T) * 8 <= 256) {  // raw rows held per lane: at most 256 bytes
 #define ZGDN_ARR_CASE(N, RR)                                                                                    \
   if (nch == N && rr == RR) {                                                                                   \
-    hipLaunchKernelGGL((attnres_reg_kernel<T, N, RR>), dim3(tokens), dim3(64 * AR_RWAVES), 0, stream, p,       \
-                       n_sources, dim, row_stride, (const T*)query, eps, (T*)out);                             \
+    hipLaunchKernelGGL((attnres_reg_kernel<T, N, RR, W>), dim3(tokens), dim3(64 * W), 0, stream, p, n_sources, \
+                       tokens,                                                                                 \
+                       dim, row_stride, (const T*)query, eps, (T*)out);                                        \
     return;                                                                                                     \
   }
-    ZGDN_ARR_CASE(1, 1) ZGDN_ARR_CASE(1, 2) ZGDN_ARR_CASE(1, 4) ZGDN_ARR_CASE(1, 8)
-    ZGDN_ARR_CASE(2, 1) ZGDN_ARR_CASE(2, 2) ZGDN_ARR_CASE(2, 4) ZGDN_ARR_CASE(2, 8)
+    ZGDN_ARR_CASE(1, 1) ZGDN_ARR_CASE(1, 2) ZGDN_ARR_CASE(1, 3) ZGDN_ARR_CASE(1, 4) ZGDN_ARR_CASE(1, 6)
+    ZGDN_ARR_CASE(1, 8) ZGDN_ARR_CASE(2, 1) ZGDN_ARR_CASE(2, 2) ZGDN_ARR_CASE(2, 3) ZGDN_ARR_CASE(2, 4)
+    ZGDN_ARR_CASE(2, 6) ZGDN_ARR_CASE(2, 8)
 #undef ZGDN_ARR_CASE
   }
   dim3 grid(tokens), block(64 * AR_WAVES);

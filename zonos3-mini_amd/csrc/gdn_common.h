@@ -86,6 +86,16 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// This wave's index in the workgroup as a wave-uniform (scalar) value: indexing by it then takes scalar
+// loads and branches (threadIdx.x >> 6 alone is a per-lane value to the compiler).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+
 // ---------------------------------------------------------------------------------------- packed sequences
 
 // Token range [bos, eos) of packed sequence s (cu_seqlens int32 [n + 1]), clamped into [0, T]: a table that
