@@ -3,10 +3,9 @@
 // x @ down.T rounded, times mask rounded, @ up rounded, added to y rounded).
 //
 // Two launches. accent_down_kernel forms tm = round(round(x . down^T) * mask) [rows, Kp] (Kp = K rounded up
-// to 32, zero columns past K) into a small workspace, and with a few more workgroups up^T [out, Kp];
-// accent_up_kernel streams y: each workgroup forms y_out = y_in + round(tm . up) for 64 rows x 128 columns
-// (y_out may be y_in). Both run on
-// bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation) for bf16; fp32 runs plain fp32 arithmetic.
+// to 32, zero columns past K) into a small workspace; accent_up_kernel streams y: each workgroup forms
+// y_out = y_in + round(tm . up) for 64-row x 128-column blocks (y_out may be y_in), reading up in place. Both
+// run on bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation) for bf16; fp32 runs plain fp32 arithmetic.
 // Every row is computed on its own in a fixed order, so a row's result never depends on the other rows of
 // the call (the batch invariance the reference gets by padding to fixed-row blocks).
 #include <algorithm>
@@ -32,111 +31,128 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// 16 bytes at p, or zeros when !ok (p must then still be a valid address).
 __device__ __forceinline__ bf16x8 load8(const uint16_t* p, bool ok) {
-  const uint4 w = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
-  return __builtin_bit_cast(bf16x8, w);
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(bf16x8, ok ? w : make_uint4(0, 0, 0, 0));
 }
 
+// Loads in both kernels are issued by every lane from clamped, always-valid addresses: a load under a lane
+// condition gets a wait for every outstanding load at its join, which would serialize the workgroup's round
+// trips. Values read for rows past the batch or columns past the output are never stored; the only loads
+// that must read as zero (the input tail when in is not a multiple of 32, up's rows past K) are selected
+// after the load.
 // tm[r][k] = round(round(sum_i x[r][i] down[k][i]) * mask[r][k]) for 16 rows per workgroup and every k < Kp.
-// Wave w sums the inputs i in its quarter of [0, in) (32 at a time, MFMA D tiles of 16 rows x 16 columns k:
-// lane holds rows 4 (l / 16) + j, column l % 16); the four partial tiles are added in wave order through
-// LDS, the same order for every row.
-// Workgroups past the row blocks write up^T [out][Kp] (zero columns past K) for the second kernel, 64 output
-// columns each, through an LDS transpose.
-__device__ __forceinline__ void transpose_up(const uint16_t* __restrict__ up, uint16_t* __restrict__ upT,
-                                             int out, int K, int n0, uint16_t* tile) {
-  const int Kp = kpad(K), pitch = Kp + 8, tid = threadIdx.x;
-  for (int e = tid; e < Kp * 8; e += 256) {  // row k, columns n0 + 8 (e % 8) .. +7
-    const int k = e / 8, c8 = (e % 8) * 8;
-    const bool ok = k < K && n0 + c8 < out;  // out is a multiple of 8
-    const uint4 w = ok ? *reinterpret_cast<const uint4*>(up + (size_t)k * out + n0 + c8) : make_uint4(0, 0, 0, 0);
-    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      tile[(c8 + 2 * j) * pitch + k] = (uint16_t)(u[j] & 0xffffu);
-      tile[(c8 + 2 * j + 1) * pitch + k] = (uint16_t)(u[j] >> 16);
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e < 64 * (Kp / 8); e += 256) {  // row n0 + n of up^T, keys 8 (e % (Kp / 8)) .. +7
-    const int n = e / (Kp / 8), k8 = (e % (Kp / 8)) * 8;
-    if (n0 + n < out)
-      *reinterpret_cast<uint4*>(upT + (size_t)(n0 + n) * Kp + k8) = *reinterpret_cast<const uint4*>(&tile[n * pitch + k8]);
-  }
-}
-
+// The input width is split over the workgroup's DW waves, each taking a contiguous run of 32-input steps
+// (MFMA D tiles of 16 rows x 16 columns k: lane holds rows 4 (l / 16) + j, column l % 16) and issuing the
+// loads of several steps at once, so that a workgroup waits about one memory round trip instead of one per
+// step; the partial tiles are added in wave order through LDS, the same order for every row. (Staging down
+// through LDS with contiguous loads, or 64 rows a workgroup sharing it, measured slower.)
+// Waves per row block: 16 up to NT = 4, then 64 / NT (the partial tiles' LDS stays at 64 KiB).
 template <int NT>
-__global__ __launch_bounds__(256) void accent_down_bf16_kernel(const uint16_t* __restrict__ x, long x_ld,
-                                                               const uint16_t* __restrict__ down,
-                                                               const uint16_t* __restrict__ mask, long mask_ld,
-                                                               uint16_t* __restrict__ tm, const uint16_t* __restrict__ up,
-                                                               uint16_t* __restrict__ upT, int rows, int in, int out,
-                                                               int K) {
-  __shared__ f32x4 part[4][NT][64];  // also the transpose tile (64 x (Kp + 8) bf16 <= 4 x NT x 64 x 16 bytes)
+constexpr int down_waves() { return NT <= 4 ? 16 : 64 / NT; }
+// input steps whose loads a wave issues at once (two for K <= 64: the 1024-input projection's 32 steps in one
+// round trip of 16 waves)
+template <int NT>
+constexpr int down_steps() { return NT >= 8 ? 1 : 8 / NT; }
+
+template <int NT, bool TAIL>  // TAIL: in is not a multiple of 32
+__global__ __launch_bounds__(64 * down_waves<NT>()) void accent_down_bf16_kernel(
+    const uint16_t* __restrict__ x, long x_ld, const uint16_t* __restrict__ down, const uint16_t* __restrict__ mask,
+    long mask_ld, uint16_t* __restrict__ tm, int rows, int in, int K) {
+  constexpr int DW = down_waves<NT>(), DSTEPS = down_steps<NT>();
+  __shared__ f32x4 part[DW][NT][64];
   const int Kp = kpad(K);
-  const int n_row_blocks = (rows + 15) / 16;
-  if ((int)blockIdx.x >= n_row_blocks) {
-    transpose_up(up, upT, out, K, ((int)blockIdx.x - n_row_blocks) * 64, reinterpret_cast<uint16_t*>(part));
-    return;
-  }
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
   const int r0 = blockIdx.x * 16;
-  const int ra = r0 + (l & 15);
-  const bool row_ok = ra < rows;
-  const int steps = (in + 31) / 32, per = (steps + 3) / 4;
+  const int ra = min(r0 + (l & 15), rows - 1);
+  const int steps = (in + 31) / 32, per = (steps + DW - 1) / DW;
   const int s0 = wave * per, s1 = min(steps, s0 + per);
+  // the mask values of this thread's output elements (see the end), read with the block's first loads
+  constexpr int FE = (16 * 16 * NT + 64 * DW - 1) / (64 * DW);  // output elements per thread, at most
+  uint16_t mk[FE];
+#pragma unroll
+  for (int j = 0; j < FE; ++j) {
+    const int e = tid + 64 * DW * j;
+    mk[j] = mask[(size_t)min(r0 + e / Kp, rows - 1) * mask_ld + min(e % Kp, K - 1)];
+  }
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int st = s0; st < s1; ++st) {
-    const int i = 32 * st + 8 * (l >> 4);
-    const bf16x8 a = load8(x + (size_t)ra * x_ld + i, row_ok && i < in);
-    bf16x8 b[NT];
+  auto batch = [&](int sb) {
+    bf16x8 a[DSTEPS], b[DSTEPS][NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int k = 16 * t + (l & 15);
-      b[t] = load8(down + (size_t)k * in + i, 16 * t < Kp && k < K && i < in);
+    for (int u = 0; u < DSTEPS; ++u) {
+      // (a step past this wave's run re-reads its last step; its products are not added)
+      const int i = 32 * min(sb + u, s1 - 1) + 8 * (l >> 4), ic = min(i, in - 8);
+      a[u] = load8(x + (size_t)ra * x_ld + ic, !TAIL || i < in);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) b[u][t] = load8(down + (size_t)min(16 * t + (l & 15), K - 1) * in + ic, true);
     }
+    // every MFMA runs (so that no load sits under a condition); a step past the run keeps the old sums, and
+    // tiles past Kp / 16 (NT = 8 with Kp = 96) are never read
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (16 * t < Kp) acc[t] = mfma_bf16(a, b[t], acc[t]);
+    for (int u = 0; u < DSTEPS; ++u) {
+      const bool live = sb + u < s1;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 r = mfma_bf16(a[u], b[u][t], acc[t]);
+        acc[t] = live ? r : acc[t];
+      }
+    }
+  };
+  // a run of at most DSTEPS steps (the 1024-input projection's) as straight-line code: in a loop the compiler
+  // keeps the loads of one iteration from overlapping the earlier ones' (waits for reused registers)
+  if (s1 - s0 <= DSTEPS) {
+    if (s0 < s1) batch(s0);
+  } else {
+    for (int sb = s0; sb < s1; sb += DSTEPS) batch(sb);
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) part[wave][t][l] = acc[t];
   __syncthreads();
-  // wave w finishes tiles t = w, w + 4, ...
-  for (int t = wave; t < NT; t += 4) {
-    if (16 * t >= Kp) break;
-    const f32x4 sum = ((part[0][t][l] + part[1][t][l]) + part[2][t][l]) + part[3][t][l];
-    const int k = 16 * t + (l & 15);
+  // thread e finishes element (row e / Kp, column e % Kp) of the block: the DW partial tiles in wave order,
+  // rounded, times the mask, rounded (columns past K: zero)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = r0 + 4 * (l >> 4) + j;
-      if (r >= rows) continue;
-      const float m = k < K ? bf16_to_f32(mask[(size_t)r * mask_ld + k]) : 0.f;
-      tm[(size_t)r * Kp + k] = f32_to_bf16(rbf(sum[j]) * m);
-    }
+  for (int j = 0; j < FE; ++j) {
+    const int e = tid + 64 * DW * j;
+    const int rl = e / Kp, k = e % Kp, r = r0 + rl, t = k >> 4, L = 16 * (rl >> 2) + (k & 15);
+    if (e >= 16 * Kp || r >= rows) break;
+    float sum = part[0][t][L][rl & 3];
+#pragma unroll
+    for (int w = 1; w < DW; ++w) sum += part[w][t][L][rl & 3];
+    tm[(size_t)r * Kp + k] = k < K ? f32_to_bf16(rbf(sum) * bf16_to_f32(mk[j])) : (uint16_t)0;
   }
 }
 
+typedef short short4_t __attribute__((ext_vector_type(4)));
+// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes, lane s supplies the address of 4
+// consecutive 16-bit elements (row k0 + s/4, columns c0 + 4 (s%4) .. +3 of a row-major matrix) and lane i
+// receives column c0 + i of rows k0 .. k0 + 3.
+__device__ __forceinline__ uint2 lds_tr(const uint16_t* p) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) short4_t*)p));
+}
+
 // y_out[r][n] = round(y_in[r][n] + round(sum_k tm[r][k] up[k][n])) for AC_RB blocks of 64 rows x 128 columns.
-// The workgroup copies its 128 rows of up^T into LDS once and walks its row blocks with the next block's y_in
-// loads in flight (16 bytes = 8 columns of one row per load, whole rows per instruction). Per block it forms
-// the products on MFMA with the output columns as the M side (A = up^T from LDS) and the rows as the N side
-// (B = tm rows), rounds them to bf16 through LDS in row order and adds them to its y values: every y access is
-// 16 contiguous bytes.
-constexpr int AC_RB = 2;  // 64-row blocks per phase-2 workgroup (the sweep over 1, 2, 4, 8: 2 best)
-template <bool HAS_Y, bool ALIGNED>
+// Every load of the workgroup is issued at its start -- its 128 columns of up (to LDS, row-major), the tm
+// fragments and the y_in values of all its row blocks (16 bytes = 8 columns of one row per load, whole rows
+// per instruction) -- so that it waits one memory round trip. Per block it forms the products on MFMA with
+// the output columns as the M side (A = up^T, read from the row-major tile with transposing LDS reads) and the
+// rows as the N side (B = tm rows), rounds them to bf16 through LDS in row order and adds them to its y
+// values: every y access is 16 contiguous bytes. KS: 32-wide adapter steps held (Kp <= 32 KS).
+constexpr int AC_RB = 2;  // 64-row blocks per phase-2 workgroup
+template <bool HAS_Y, bool ALIGNED, int KS>
 __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __restrict__ tm,
-                                                             const uint16_t* __restrict__ upT,
+                                                             const uint16_t* __restrict__ up,
                                                              const uint16_t* y_in, long y_in_ld,
                                                              uint16_t* y_out, long y_out_ld, int rows,
                                                              int out, int K) {  // y_out may equal y_in
-  constexpr int NB = AC_NB, SP = NB + 8;
-  extern __shared__ uint16_t lds[];  // up^T tile [NB][Kp + 8], then the products [AC_ROWS][SP]
-  const int Kp = kpad(K), pitch = Kp + 8;
+  constexpr int NB = AC_NB, SP = NB + 8;  // (row pitch of both LDS tiles: 272 bytes)
+  extern __shared__ uint16_t lds[];        // up's tile [Kp][SP] (rows k, columns n0 ..), the products [AC_ROWS][SP]
+  const int Kp = kpad(K);
   uint16_t* ut = lds;
-  uint16_t* sh = lds + NB * pitch;
+  uint16_t* sh = lds + Kp * SP;
   // Workgroup ids go round-robin over the 8 XCDs: all column blocks of one row block take ids of one residue
   // mod 8, so they run on one XCD and share its L2 copy of the 128-byte lines their rows straddle (the
   // projection's rows are rarely line-aligned: 2056 bf16 = 4112 bytes).
@@ -145,50 +161,72 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
   const int rblk = (slot / n_nb) * 8 + xcd, nblk = slot % n_nb;
   if (rblk >= n_rb) return;
   const int n0 = nblk * NB, rbase = rblk * (AC_ROWS * AC_RB);
-  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, l = tid & 63, wave = wave_id();
   constexpr int G = NB / 8;               // 16-byte groups per row of y
   constexpr int PER = AC_ROWS * G / 256;  // y groups per thread and block
-  auto load_y = [&](int r0, uint4* yw) {
+  constexpr int NT = NB / 16;
+  // up rows k < Kp, columns n0 .. n0 + NB - 1 (for LDS: zeros past K, where tm is zero too, keep non-finite
+  // values of up's last row out), loaded first so that their stores to LDS wait for these loads only
+  constexpr int UPER = 32 * KS * G / 256;
+  uint4 uw[UPER];
+#pragma unroll
+  for (int it = 0; it < UPER; ++it) {
+    const int e = tid + 256 * it, k = e / G, c8 = 8 * (e % G);
+    uw[it] = *reinterpret_cast<const uint4*>(up + (size_t)min(k, K - 1) * out + min(n0 + c8, out - 8));
+  }
+  // then y_in of every block and the tm fragments of every block (wave w: rows 16 w .. +15 of each block, the
+  // MFMA N side)
+  uint4 yw[AC_RB][PER];
+  bf16x8 tb[AC_RB][KS];
+#pragma unroll
+  for (int b = 0; b < AC_RB; ++b) {
+    const int r0 = rbase + AC_ROWS * b;
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int e = tid + 256 * p, r = r0 + e / G, n = n0 + 8 * (e % G);
-      yw[p] = make_uint4(0, 0, 0, 0);
-      if (HAS_Y && r < rows && n < out) {
-        const uint16_t* yp = y_in + (size_t)r * y_in_ld + n;
+      yw[b][p] = make_uint4(0, 0, 0, 0);
+      if constexpr (HAS_Y) {
+        const uint16_t* yp = y_in + (size_t)min(r, rows - 1) * y_in_ld + min(n, out - 8);
         if constexpr (ALIGNED) {
-          yw[p] = *reinterpret_cast<const uint4*>(yp);
+          yw[b][p] = *reinterpret_cast<const uint4*>(yp);
         } else {
           uint32_t u[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) u[j] = (uint32_t)yp[2 * j] | ((uint32_t)yp[2 * j + 1] << 16);
-          yw[p] = make_uint4(u[0], u[1], u[2], u[3]);
+          yw[b][p] = make_uint4(u[0], u[1], u[2], u[3]);
         }
       }
     }
-  };
-  uint4 ya[PER], yb[PER];
-  load_y(rbase, ya);
-  for (int e = tid; e < NB * (Kp / 8); e += 256) {  // up^T rows n0 .. n0 + NB - 1 into LDS
-    const int n = e / (Kp / 8), k8 = (e % (Kp / 8)) * 8;
-    const uint4 w = n0 + n < out ? *reinterpret_cast<const uint4*>(upT + (size_t)(n0 + n) * Kp + k8)
-                                 : make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(&ut[n * pitch + k8]) = w;
+    const int rb = min(r0 + 16 * wave + (l & 15), rows - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) tb[b][ks] = load8(tm + (size_t)rb * Kp + min(32 * ks + 8 * (l >> 4), Kp - 8), true);
+  }
+#pragma unroll
+  for (int it = 0; it < UPER; ++it) {
+    const int e = tid + 256 * it, k = e / G, c8 = 8 * (e % G);
+    if (k < Kp) *reinterpret_cast<uint4*>(&ut[k * SP + c8]) = k < K ? uw[it] : make_uint4(0, 0, 0, 0);
   }
   __syncthreads();
 
-  constexpr int NT = NB / 16;
-  auto block = [&](int r0, const uint4* yw) {
-    // wave w: rows r0 + 16 w .. +15 (MFMA N side), all NB columns
-    const int rb = r0 + 16 * wave + (l & 15);
+#pragma unroll
+  for (int b = 0; b < AC_RB; ++b) {
+    const int r0 = rbase + AC_ROWS * b;
+    if (r0 >= rows) break;
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < Kp; k0 += 32) {
-      const int kk = k0 + 8 * (l >> 4);
-      const bf16x8 b = load8(tm + (size_t)rb * Kp + kk, rb < rows);
+    const int sl = l & 15;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[t] = mfma_bf16(*reinterpret_cast<const bf16x8*>(&ut[(16 * t + (l & 15)) * pitch + kk]), b, acc[t]);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (32 * ks >= Kp) break;
+      // A fragment: column n0 + 16 t + l % 16 of up, k = 32 ks + 8 (l / 16) .. +7 (two transposing reads)
+      const int k0 = 32 * ks + 8 * (l >> 4) + (sl >> 2);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint2 a0 = lds_tr(&ut[k0 * SP + 16 * t + 4 * (sl & 3)]);
+        const uint2 a1 = lds_tr(&ut[(k0 + 4) * SP + 16 * t + 4 * (sl & 3)]);
+        acc[t] = mfma_bf16(__builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y)), tb[b][ks], acc[t]);
+      }
     }
     // D: lane holds columns 16 t + 4 (l / 16) + j of row 16 w + l % 16: rounded products to LDS
     const int rr = 16 * wave + (l & 15);
@@ -204,7 +242,7 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
       const int e = tid + 256 * p, rl = e / G, cl = 8 * (e % G), r = r0 + rl, n = n0 + cl;
       if (r >= rows || n >= out) continue;
       const uint4 sw = *reinterpret_cast<const uint4*>(&sh[rl * SP + cl]);
-      const uint32_t su[4] = {sw.x, sw.y, sw.z, sw.w}, yu[4] = {yw[p].x, yw[p].y, yw[p].z, yw[p].w};
+      const uint32_t su[4] = {sw.x, sw.y, sw.z, sw.w}, yu[4] = {yw[b][p].x, yw[b][p].y, yw[b][p].z, yw[b][p].w};
       uint32_t ou[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -223,18 +261,7 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
         }
       }
     }
-    __syncthreads();  // the products' LDS is rewritten by the next block
-  };
-  // blocks alternate between the two y buffers, the next block's loads issued before the current one's work
-#pragma unroll
-  for (int b = 0; b < AC_RB; b += 2) {
-    const int r0 = rbase + AC_ROWS * b;
-    if (r0 >= rows) break;
-    load_y(r0 + AC_ROWS, yb);
-    block(r0, ya);
-    if (r0 + AC_ROWS >= rows) break;
-    if (b + 2 < AC_RB) load_y(r0 + 2 * AC_ROWS, ya);
-    block(r0 + AC_ROWS, yb);
+    if (b + 1 < AC_RB) __syncthreads();  // the products' LDS is rewritten by the next block
   }
 }
 
@@ -273,8 +300,8 @@ __global__ __launch_bounds__(256) void accent_up_f32_kernel(const float* __restr
 extern "C" size_t zgdn_accent_workspace_size(int rows, int out, int K, int dtype) {
   if (rows <= 0 || out <= 0 || K <= 0) return 0;
   const size_t Kp = (size_t)((K + 31) / 32 * 32);
-  // tm [rows, Kp]; bf16 also up^T [out, Kp]
-  return dtype == ZGDN_F32 ? (size_t)rows * Kp * 4 : ((size_t)rows + (size_t)out) * Kp * 2;
+  // tm [rows, Kp]
+  return (size_t)rows * Kp * (dtype == ZGDN_F32 ? 4 : 2);
 }
 
 extern "C" int zgdn_accent_shift(const void* x, long x_ld, const void* down, const void* up, const void* mask,
@@ -302,16 +329,15 @@ extern "C" int zgdn_accent_shift(const void* x, long x_ld, const void* down, con
   hipStream_t s = (hipStream_t)stream;
   const int Kp = (K + 31) / 32 * 32;
   if (bf) {
-    // row blocks of 16, then one workgroup per 64 output columns writing up^T
-    const dim3 g1((rows + 15) / 16 + (out + 63) / 64);
+    const dim3 g1((rows + 15) / 16);  // row blocks of 16
     auto d = (const uint16_t*)down;
     auto m = (const uint16_t*)mask;
     auto tm = (uint16_t*)workspace;
-    auto upT = tm + (size_t)rows * Kp;
     auto go1 = [&](auto nt) {
       constexpr int NT = decltype(nt)::value;  // MFMA column tiles per wave, Kp / 16 rounded up to a power of 2
-      hipLaunchKernelGGL(accent_down_bf16_kernel<NT>, g1, dim3(256), 0, s, (const uint16_t*)x, x_ld, d, m, mask_ld,
-                         tm, (const uint16_t*)up, upT, rows, in, out, K);
+      auto k1 = in % 32 ? accent_down_bf16_kernel<NT, true> : accent_down_bf16_kernel<NT, false>;
+      hipLaunchKernelGGL(k1, g1, dim3(64 * down_waves<NT>()), 0, s, (const uint16_t*)x, x_ld, d, m, mask_ld, tm, rows,
+                         in, K);
     };
     if (Kp <= 32) go1(std::integral_constant<int, 2>{});
     else if (Kp <= 64) go1(std::integral_constant<int, 4>{});
@@ -321,14 +347,20 @@ extern "C" int zgdn_accent_shift(const void* x, long x_ld, const void* down, con
                          (y_in == nullptr || y_in_ld % 8 == 0);
     const int n_nb = (out + AC_NB - 1) / AC_NB, n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
     const dim3 g2(8 * n_nb * ((n_rb + 7) / 8));  // XCD-grouped ids (see the kernel)
-    const size_t lds = ((size_t)AC_NB * (Kp + 8) + (size_t)AC_ROWS * (AC_NB + 8)) * 2;  // <= 84,992 bytes
-    auto up2 = y_in != nullptr ? (aligned ? accent_up_bf16_kernel<true, true> : accent_up_bf16_kernel<true, false>)
-                               : (aligned ? accent_up_bf16_kernel<false, true> : accent_up_bf16_kernel<false, false>);
+    const size_t lds = ((size_t)Kp + AC_ROWS) * (AC_NB + 8) * 2;  // <= 87,040 bytes
+    auto pick = [&](auto ks) -> void (*)(const uint16_t*, const uint16_t*, const uint16_t*, long, uint16_t*, long,
+                                         int, int, int) {
+      constexpr int KS = decltype(ks)::value;
+      return y_in != nullptr
+                 ? (aligned ? accent_up_bf16_kernel<true, true, KS> : accent_up_bf16_kernel<true, false, KS>)
+                 : (aligned ? accent_up_bf16_kernel<false, true, KS> : accent_up_bf16_kernel<false, false, KS>);
+    };
+    auto up2 = Kp <= 64 ? pick(std::integral_constant<int, 2>{}) : pick(std::integral_constant<int, 8>{});
     if (lds > 65536 &&
         hipFuncSetAttribute((const void*)up2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return fail(ZGDN_EHIP, "%s: %zu bytes of LDS for K=%d not available", fn, lds, K);
-    hipLaunchKernelGGL(up2, g2, dim3(256), lds, s, tm, upT, (const uint16_t*)y_in, y_in_ld, (uint16_t*)y_out,
-                       y_out_ld, rows, out, K);
+    hipLaunchKernelGGL(up2, g2, dim3(256), lds, s, tm, (const uint16_t*)up, (const uint16_t*)y_in, y_in_ld,
+                       (uint16_t*)y_out, y_out_ld, rows, out, K);
   } else {
     auto tm = (float*)workspace;
     const long n1 = (long)rows * Kp, n2 = (long)rows * out;
