@@ -253,8 +253,8 @@ int zgdn_gated_rmsnorm_fwd(const void* x, const void* g, const void* weight, int
                            int rows, int D, int g_group, long g_ld, float eps, void* stream);
 
 /*
- * Bytes of workspace zgdn_accent_shift needs: (rows + out) x K rounded up to 32 bf16 elements (bf16), rows x K
- * rounded up to 32 floats (fp32).
+ * Bytes of workspace zgdn_accent_shift needs: rows x K rounded up to 32, of bf16 elements (bf16) or floats
+ * (fp32).
  */
 size_t zgdn_accent_workspace_size(int rows, int out, int K, int dtype);
 
