@@ -191,3 +191,60 @@ def test_plan_extend_splits_each_joined_run_at_its_last_chunk(serving):
     assert open_.dest == list(range(64, 70)) + [124, 125] and open_.out_rows == [0, 1, 2, 3, 4, 5, 9, 10]
     assert open_.window == [2 * 64 + j for j in range(6)] + [3 * 64 + j for j in range(5)]
     assert open_.member_of_row == [0] * 6 + [2] * 5
+
+
+def test_static_prefill_bookkeeping(serving):
+    """A padded static prefill (PrefillLayout of complete-chunk counts 0, 2, 1) with the packed pass replaced by
+    ``_transparent_packed`` (extended with a projection stand-in, mixed = x tiled to the in_proj width):
+    outputs of complete chunks and windows land on their batch rows, committed states hold the complete
+    chunks' rows, live states all real rows (the padding rows' values are zeroed first, and their gate inputs
+    set to the no-op values), windows keep the rows with their real count in win_len, and the live conv
+    history is the last CONV_WIDTH projection rows before the padding, the committed history in front."""
+    hid = 8
+    batch = SimpleNamespace(is_decode=False, padded_size=0)
+    layer = serving.OriginalGDN(SimpleNamespace(hidden_size=hid), layer_id=2, batch_source=lambda: batch)
+    layer.allocate_cache(4, torch.device("cpu"), torch.float64)
+    calls = []
+    base = _transparent_packed(calls)
+    seen = {}
+
+    def run(x, cu, chunks, conv, recurrent, mask=None, valid=None, return_mixed=False):
+        if valid is not None:
+            seen["valid"] = valid.clone()
+            assert torch.equal(x[~valid], torch.zeros_like(x[~valid]))  # padding rows arrive zeroed
+        out, conv_final, final = base(x, cu, chunks, conv, recurrent)[:3]
+        if valid is not None:  # decay 1, beta 0: the padding rows leave the states alone
+            sums = torch.stack([p[v].sum() for p, v in zip(x.split((cu[1:] - cu[:-1]).tolist()),
+                                                           valid.split((cu[1:] - cu[:-1]).tolist()))])
+            final = recurrent + sums.view(-1, 1, 1, 1)
+        mixed = x.repeat(1, -(-2056 // hid))[:, :2056]
+        return (out, conv_final, final, mixed) if return_mixed else (out, conv_final, final)
+
+    layer._run_packed = run
+    whole, lengths, slots = [0, 2, 1], [5, 130, 64], [2, 0, 3]
+    layout = serving.PrefillLayout.build(whole, torch.device("cpu"))
+    rows = sum(64 * (w + 1) for w in whole)
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(rows, hid, generator=gen, dtype=torch.float64)
+    batch.gdn_prefill = serving.PrefillInputs(layout, torch.tensor(slots), torch.tensor(lengths))
+    y = layer.forward(x)
+    start = 0
+    for w, n, s in zip(whole, lengths, slots):
+        seg = x[start:start + 64 * (w + 1)]
+        real = seg[:n]
+        done = 64 * w
+        if done:  # the complete chunks: one packed sequence from zero states, outputs row + position
+            assert torch.equal(y[start:start + done], seg[:done] + torch.arange(done, dtype=x.dtype).view(-1, 1))
+        fill = n - done
+        win_out = y[start + done:start + done + fill]
+        assert torch.equal(win_out, seg[done:n] + torch.arange(fill, dtype=x.dtype).view(-1, 1))
+        assert torch.allclose(layer._conv_state[s], real[:done].sum().expand(1536, 4))
+        assert torch.allclose(layer._recurrent_state[s], real[:done].sum().expand(4, 128, 128).float())
+        assert torch.allclose(layer._live_state[s], real.sum().expand(4, 128, 128).float())
+        assert layer._win_len[s].item() == fill
+        assert torch.equal(layer._window[s, :fill], seg[done:n])
+        # live conv: the last 4 conv inputs up to the window's last real row, the committed history first
+        hist = torch.cat((layer._conv_state[s], seg[done:n].repeat(1, -(-2056 // hid))[:, :1536].T), dim=1)
+        assert torch.equal(layer._live_conv[s], hist[:, fill:fill + 4])
+        start += 64 * (w + 1)
+    assert seen["valid"].view(3, 64).sum(1).tolist() == [n - 64 * w for w, n in zip(whole, lengths)]
