@@ -55,10 +55,10 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
 
 /*
  * Bytes of workspace zgdn_chunk_fwd needs for n_chunks 64-token chunks (over all sequences) and Hv value
- * heads: 98,560 bytes per chunk and head, then the control block of the overlapped launch (3,328 bytes and 4
+ * heads: 98,560 bytes per chunk and head, then the control block of the overlapped launch (11,520 bytes and 4
  * per chunk and head, padded to 256). zgdn_chunk_fwd runs phase 1 (per chunk) and the sequential state pass
  * in one launch, side by side, where that measured faster than two launches: one sequence of 16 heads and
- * 4096 tokens and similar (8 .. 32 (sequence, head) chains of 64 chunks or more), and packed or batched
+ * 4096 tokens and similar (8 .. 16 (sequence, head) chains of 64 chunks or more), and packed or batched
  * sequences with at least 3072 chunk x head items and 8 chunks or more per chain on average (up to 256 packed
  * sequences). zgdn_chunk_set_launch_form overrides that choice (the same results, bit for bit).
  */

@@ -97,8 +97,9 @@ def test_bad_arguments_fail_with_a_message(gdn):
     assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=64" in lib.zgdn_last_error()
     chunk[21], chunk[3] = 128, 0  # fp32 q/k/v
     assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"bf16" in lib.zgdn_last_error()
-    # items, then the control block of the overlapped launch (13 x 256 bytes + one 4-byte flag per item)
-    assert lib.zgdn_chunk_workspace_size(64, 16) == 64 * 16 * 98560 + 256 * 13 + 64 * 16 * 4
+    # items, then the control block of the overlapped launch (45 x 256 bytes: tickets, per-CU arrival counts;
+    # then one 4-byte flag per item)
+    assert lib.zgdn_chunk_workspace_size(64, 16) == 64 * 16 * 98560 + 256 * 45 + 64 * 16 * 4
     # conv width, state width; row-op sizes; fused block group size
     conv = [p, p, None, 1, None, None, 4, p, None, None, 1, 0, 1, 8, 16, 5, 1, 16, None]
     assert lib.zgdn_causal_conv1d_fwd(*conv) == native.EUNSUPPORTED and b"width 5" in lib.zgdn_last_error()

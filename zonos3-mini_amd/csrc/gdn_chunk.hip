@@ -724,12 +724,12 @@ struct StateArgs {
   const uint8_t* ws;
   int c0, bos, len, nchunks, Hv, h, vb;
   float xs;  // 1, or 0 for a transition run (Ub' and Ob taken as zero: the pass then carries S -> S A_c)
-  // overlapped form: the ready flag of item (chunk c, head h) is flags[c * Hv + h], nonzero once phase 1
-  // has stored the item; spin_max bounds each wait (never_ready: every flag reads as unready, so each wait
-  // runs out -- the host's test of the error path)
-  int* flags;
+  // overlapped form: the ready flag of this job's chunk ci is flags[ci * flag_step], nonzero once phase 1 has
+  // stored the item (flag_step 0 with flags on a word that stays zero: every wait runs out -- the host's test
+  // of the error path); spin_max bounds each wait
+  const int* flags;
+  int flag_step;
   int spin_max;
-  int never_ready;
 };
 
 // Default bound on a state pass's wait for one item (a few tenths of a second): a wait that runs out sets bit
@@ -814,7 +814,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   // the flag's round trip is hidden when phase 1 is ahead) and issue the read of the next one's.
   if (a.nchunks <= 0) return;
   const int last = a.nchunks - 1;
-  const int* fbase = Wait ? a.flags + (size_t)a.c0 * a.Hv + a.h : nullptr;
+  const int* fbase = Wait ? a.flags : nullptr;
   int fl = 0;
   bool gave_up = false;
   auto wait_ready = [&](int ni) {
@@ -829,10 +829,10 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
           break;
         }
         __builtin_amdgcn_s_sleep(2);
-        f = a.never_ready ? 0 : load_flag(fbase + (size_t)ni * a.Hv);
+        f = load_flag(fbase + (size_t)ni * a.flag_step);
       }
       asm volatile("" ::: "memory");  // the chunk's loads stay behind the wait
-      fl = a.never_ready ? 0 : load_flag(fbase + (size_t)min(ni + 1, last) * a.Hv);
+      fl = load_flag(fbase + (size_t)min(ni + 1, last) * a.flag_step);
     }
   };
 
@@ -988,8 +988,8 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 
   TOut* out = trans ? reinterpret_cast<TOut*>(seg.trans_out) : o;
   a.flags = nullptr;
+  a.flag_step = 0;
   a.spin_max = 0;
-  a.never_ready = 0;
   if (wave < 4)
     state_loop<true, TOut, false>(sh, a, out, S);
   else
@@ -1025,19 +1025,29 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 // Producer and consumers of a chunk's workspace must share one L2: the XCDs' L2 caches are not coherent with
 // each other, and the fences that would make them so write back or drop a whole L2. So every chain belongs to
 // one queue, chain % n_q, and a workgroup serves the queue of the XCD it runs on (the hardware XCC_ID
-// register). Each workgroup takes one role when it arrives (role ticket of its queue): state worker or item
-// worker. Item workers take the queue's items from an item ticket in a fixed order until none are left; state
-// workers take its state jobs (chain x 8 value blocks, chains in queue order) from a state ticket. An item's
-// workgroup sets the item's ready flag once its workspace stores have reached the L2; a state job reads each
-// chunk's flag (one chunk ahead) before its loads. No data of a chunk is in any L1 before its flag is set (only
-// state jobs read the workspace, and only after the flag), so plain loads see the stores through the shared L2.
-//   few chains (at most FQ_FEW_CHAINS a queue, unpacked): the first nch arrivals take items, the next 8 nch one
-//     state job each, the rest items; items in chunk order across the queue's chains.
-//   many chains: the first arrival takes items, the next FQ_STATE_WORKERS state jobs one after another, the
-//     rest items; items chain after chain, so state jobs start in the order their chains are produced.
+// register). Each workgroup takes one role when it arrives: state worker or item worker. Item workers take the
+// queue's items from an item ticket in a fixed order until none are left; state workers take its state jobs
+// (chain x 8 value blocks, chains in queue order) from a state ticket. An item's workgroup sets the item's
+// ready flag once its workspace stores have reached the L2; a state job reads each chunk's flag (one chunk
+// ahead) before its loads. No data of a chunk is in any L1 before its flag is set (only state jobs read the
+// workspace, and only after the flag), so plain loads see the stores through the shared L2.
+// Roles go by placement, not by arrival order: the queue's first arrival takes items; a later workgroup takes
+// a state role if it is the first to arrive on its CU (per-CU arrival count, keyed by XCC_ID and the HW_ID
+// register's shader engine, array and CU) and the queue's state roles (8 nch for few chains, FQ_STATE_WORKERS
+// for many) are not all taken; every other workgroup takes items. The dispatcher puts workgroups b and
+// b + n_cu on one CU and arrivals only roughly follow blockIdx, so roles by arrival put two state workgroups on
+// one CU now and then; the second then finished its chain 20-30 us after every other (T = 4096, 16 heads:
+// the kernel's 82-99 us against 71-76 us for the rest).
+//   few chains (at most FQ_FEW_CHAINS a queue, unpacked): one state job each; items in chunk order across the
+//     queue's chains.
+//   many chains: state jobs one after another; items chain after chain, so state jobs start in the order
+//     their chains are produced.
 // Progress: items never wait and every queue's first arrival takes items, so every item is stored whatever the
-// number of resident workgroups; a wait that runs out (the spin bound) sets the device status word and the kernel still ends.
-// The control block (per-queue tickets, one flag per item) is zeroed before each launch.
+// number of resident workgroups; the queue's second arrival is the first to claim its CU (the first arrival
+// claims none), so every queue of two or more workgroups (the grid gives each about 2 per CU of its XCD) has a
+// state worker, and state workers take jobs until none are left. A wait that runs out (the spin bound) sets the
+// device status word and the kernel still ends.
+// The control block (per-queue tickets, per-CU arrival counts, one flag per item) is zeroed before each launch.
 constexpr int FQ_MAX = 8;              // queues (one per XCD)
 constexpr int FQ_FEW_CHAINS = 4;       // chains per queue of the few-chains order (32 state workgroups of 64)
 constexpr int FQ_STATE_WORKERS = 24;   // workgroups per queue taking state jobs in the many-chains order
@@ -1045,15 +1055,23 @@ constexpr int FQ_MAX_SEQS = 256;       // packed sequences (LDS table of chunk o
 constexpr int FQ_MAX_QCHAINS = 512;    // chains per queue in the many-chains order (LDS table)
 
 struct FusedCtl {
-  int* tickets;  // queue q: role ticket at [96 q], item ticket at [96 q + 32], state ticket at [96 q + 64]
-  int* flags;    // [n_items]
+  // queue q: role ticket at [96 q], state-role count at [96 q + 16], item ticket at [96 q + 32], state
+  // ticket at [96 q + 64]
+  int* tickets;
+  int* cu_claims;  // [FQ_CU_KEYS]: arrivals per CU (key of cu_key)
+  int* flags;      // [n_items]
   int n_q;       // queues in use (XCDs of the device)
   int few;       // few-chains order
   int spin_max;  // bound of each wait for a ready flag
-  int never_ready;
+  int never_ready;  // state jobs read a zero word in place of their flags (the wait's error path)
 };
 
-constexpr size_t FQ_HEADER = 256 * 13;  // tickets (8 queues x 3 lines of 128 bytes), then padding
+constexpr int FQ_ZERO_WORD = 96 * FQ_MAX;  // the int after the tickets: zeroed with the block, never written
+constexpr int FQ_CU_KEYS = 8 * 256;        // CU keys: XCD (3 bits) x shader engine, array, CU (HW_ID bits 15:8)
+constexpr int FQ_CLAIMS = 832;             // int offset of the per-CU arrival counts (after 256 B of padding)
+// tickets (8 queues x 3 lines of 128 bytes), the zero word and padding, the per-CU arrival counts
+constexpr size_t FQ_HEADER = 4 * ((size_t)FQ_CLAIMS + FQ_CU_KEYS);
+static_assert(FQ_HEADER % 256 == 0 && FQ_ZERO_WORD < FQ_CLAIMS, "control block layout");
 size_t fused_ctl_bytes(int n_items) { return FQ_HEADER + (((size_t)n_items * 4 + 255) / 256) * 256; }
 
 __global__ void zero_ints_kernel(int* p, int n) {
@@ -1136,14 +1154,23 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
   auto chunk0 = [&](int sq) { return cu != nullptr ? seq_c0[sq] : sq * nct_t; };
   const int n_q_items = ctl.few ? nch * nct_t : qpref[nch];
 
-  // role
-  if (threadIdx.x == 0) tk = __hip_atomic_fetch_add(ctl.tickets + 96 * qi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const int role = tk;
-  const int n_first = ctl.few ? nch : 1;
+  // role (state or items)
   const int n_workers = ctl.few ? n_state : min(n_state, FQ_STATE_WORKERS);
+  if (threadIdx.x == 0) {
+    int state = 0;
+    if (__hip_atomic_fetch_add(ctl.tickets + 96 * qi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) > 0) {
+      unsigned hw;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+      const int key = ((xcc & 7) << 8) | (int)((hw >> 8) & 0xff);  // XCD, shader engine, array, CU
+      if (__hip_atomic_fetch_add(ctl.cu_claims + key, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+          __hip_atomic_fetch_add(ctl.tickets + 96 * qi + 16, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n_workers)
+        state = 1;
+    }
+    tk = state;
+  }
+  __syncthreads();
 
-  if (role >= n_first && role < n_first + n_workers) {
+  if (tk != 0) {
     const int l = lane_id(), wave = threadIdx.x >> 6;
     __builtin_amdgcn_s_setprio(3);  // the sequential pass's waves issue ahead of phase-1 waves on their CU
     for (;;) {
@@ -1165,9 +1192,11 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
       a.len = seq_len(sq);
       a.c0 = chunk0(sq);
       a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
-      a.flags = ctl.flags;
+      // (never_ready: the job reads the zero word in place of its flags; applying the test to the flag values
+      // instead puts a wait for each prefetched flag right behind its load)
+      a.flags = ctl.never_ready ? ctl.tickets + FQ_ZERO_WORD : ctl.flags + (size_t)a.c0 * Hv + h;
+      a.flag_step = ctl.never_ready ? 0 : Hv;
       a.spin_max = ctl.spin_max;
-      a.never_ready = ctl.never_ready;
       const int ncol = 16 * wave + (l & 15);
       const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
       const size_t hs = (size_t)DV * DK;
@@ -1448,18 +1477,20 @@ std::atomic<int> g_spin_max{SPIN_MAX};
 std::atomic<int> g_never_ready{0};
 
 // Whether an eligible batch takes the overlapped launch: as the launch form says, or (the library's choice)
-// where it measured faster than the two launches
-// on MI355X (same-process comparisons, bf16, dk = dv = 128): few chains only with long sequences (64 chunks:
-// 82.6 against 84.6 us; at 8 .. 32 chunks it was 15-45 % slower), many chains when there are at least 3072
-// chunk x head items and 8 chunks or more per chain on average (+3-11 %: 512 chains of 8 chunks, 256 of 12 or
-// 16, 128 of 32, the 32-sequence packed workload); 256 chains of 8, 128 of 16, 64 of 32 lost 2-15 % (the state
+// where it measured faster than the two launches on MI355X (same-process comparisons, bf16, dk = dv = 128, us
+// overlapped / two launches): few chains only with long sequences and at most 2 chains a queue (16 chains of
+// 64 chunks 80.7 / 82.8, 8 of 64 56.5 / 56.5; 16 of 32, 16, 8 chunks 51.2 / 45.1, 34.4 / 29.0, 27.6 / 21.1;
+// 32 of 64 -- 4 a queue, whose 32 state workgroups take every CU of the XCD -- 193.2 / 143.4), many chains
+// when there are at least 3072 chunk x head items and 8 chunks or more per chain on average (512 chains of 8
+// chunks 304.8 / 336.1, 256 of 12 233.5 / 252.9, 256 of 16 312.2 / 330.5, 128 of 32 312.4 / 328.7, the
+// 32-sequence packed workload 559.4 / 633.9); 64 chains of 32 lost (166.9 / 148.5), 256 of 8 tied (the state
 // pass starts only after the first items, shares its CUs with phase 1, and with a fixed share of state
 // workgroups short or few chains leave them waiting).
-bool overlap_wanted(bool few, long n_items, double chunks_per_chain) {
+bool overlap_wanted(bool few, long n_items, double chunks_per_chain, long chains_per_queue) {
   const int form = g_launch_form.load(std::memory_order_relaxed);
   if (form == 0) return false;
   if (form == 1) return true;
-  if (few) return chunks_per_chain >= 64;
+  if (few) return chunks_per_chain >= 64 && chains_per_queue <= 2;
   return n_items >= 3072 && chunks_per_chain >= 8;
 }
 
@@ -1593,8 +1624,8 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
     p += (size_t)B * (plan.G - 1) * Hv * hs * 4;
     s_start = reinterpret_cast<uint16_t*>(p);
   }
-  // phases 1 and 2 in one overlapped launch where it pays (overlap_wanted): unpacked batches of 8 .. 32 chains
-  // (few-chains order) on the plain pass, packed batches of up to 256 sequences and unpacked batches of more
+  // phases 1 and 2 in one overlapped launch where it pays (overlap_wanted): unpacked batches of 8 .. 16 long
+  // chains (few-chains order) on the plain pass, packed batches of up to 256 sequences and unpacked batches of more
   // chains (many-chains order)
   const int n_q = std::min(FQ_MAX, std::max(1, device_cus() / 32));  // XCDs (32 CUs each on gfx950)
   const long n_chains = (long)N * Hv;
@@ -1602,10 +1633,10 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
   const bool fits = few || ((cu_seqlens == nullptr || N <= FQ_MAX_SEQS) &&
                             (n_chains + n_q - 1) / n_q <= FQ_MAX_QCHAINS);
   if (!segmented && n_chunks > 0 && n_chains >= n_q && fits &&
-      overlap_wanted(few, (long)n_chunks * Hv, (double)n_chunks / std::max(1, N))) {
+      overlap_wanted(few, (long)n_chunks * Hv, (double)n_chunks / std::max(1, N), (n_chains + n_q - 1) / n_q)) {
     const int n_items = n_chunks * Hv;
     int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
-    const FusedCtl ctl{ctl_base, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0,
+    const FusedCtl ctl{ctl_base, ctl_base + FQ_CLAIMS, ctl_base + FQ_HEADER / 4, n_q, few ? 1 : 0,
                        g_spin_max.load(std::memory_order_relaxed), g_never_ready.load(std::memory_order_relaxed)};
     const int n_ctl = (int)(fused_ctl_bytes(n_items) / 4);
     hipLaunchKernelGGL(zero_ints_kernel, dim3((n_ctl + 255) / 256), dim3(256), 0, s, ctl_base, n_ctl);
