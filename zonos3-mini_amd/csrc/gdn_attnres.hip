@@ -18,6 +18,8 @@ namespace zgdn {
 namespace {
 
 constexpr int AR_WAVES = 4;
+
+
 constexpr int AR_MAX_SOURCES = 64;
 
 struct SourcePtrs {
@@ -249,63 +251,122 @@ struct MixSm {
   float logit[AR_MAX_SOURCES];
 };
 
+// The cross-lane sums of R per-lane values at once: each v[j] becomes the sum over the wave's 64 lanes, as a
+// wave-uniform value. Row sums by DPP; then the gfx950 permlane swaps, shared by 2 or 4 values: a 16-lane swap of
+// a and b leaves a's row-pair sums in rows 0 and 2 and b's in rows 1 and 3, a 32-lane swap of two such results
+// leaves four totals in rows 0-3, read with readlane. Each total is (s0 + s1) + (s2 + s3) of its row sums, the
+// value wave_sum forms.
+template <int R>
+__device__ __forceinline__ void wave_sums(float (&v)[R]) {
+#pragma unroll
+  for (int j = 0; j < R; ++j) v[j] = group_sum<16>(v[j]);
+  auto pair16 = [](float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  };
+  auto pair32 = [](float a, float b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  };
+  auto at = [](float x, int l) { return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(x), l)); };
+  int j = 0;
+#pragma unroll
+  for (; j + 4 <= R; j += 4) {
+    const float t = pair32(pair16(v[j], v[j + 1]), pair16(v[j + 2], v[j + 3]));
+    v[j] = at(t, 0);
+    v[j + 1] = at(t, 16);
+    v[j + 2] = at(t, 32);
+    v[j + 3] = at(t, 48);
+  }
+  if constexpr (R % 4 >= 2) {
+    const float ab = pair16(v[R / 4 * 4], v[R / 4 * 4 + 1]), t = pair32(ab, ab);
+    v[R / 4 * 4] = at(t, 0);
+    v[R / 4 * 4 + 1] = at(t, 16);
+  }
+  if constexpr (R % 2 == 1) {
+    const float a = pair16(v[R - 1], v[R - 1]), t = pair32(a, a);
+    v[R - 1] = at(t, 0);
+  }
+}
+
 // One token's mix from its rows in registers. Two workgroup barriers: after the logits (before the softmax
-// reads them) and after the partial mixes (before the final sums read them).
-template <typename T, int NCH, int R, int W>
+// reads them) and after the partial mixes (before the final sums read them). FULL: dim == 512 NCH (every
+// lane's pieces are columns of the row; no per-piece tests).
+template <typename T, int NCH, int R, int W, bool FULL>
 __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const QueryRegs<T, NCH> qr,
                                           MixSm<T, NCH, R, W>& sm, int n_sources, int dim, float eps, int token,
                                           int wave, int lane, T* __restrict__ out) {
   bool on[NCH];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) on[c] = 8 * (lane + 64 * c) < dim;
+  for (int c = 0; c < NCH; ++c) on[c] = FULL || 8 * (lane + 64 * c) < dim;
   const float inv_dim = 1.f / (float)dim;
-  // pass 1: logit_s = sum round(round(x r) q), r = rsqrt(mean(x^2) + eps)
+  // pass 1: logit_s = sum round(round(x r) q), r = rsqrt(mean(x^2) + eps). Every owned slot is computed (a slot
+  // past the last source holds that source's row again: finite values, never stored), so that the slots'
+  // cross-lane sums run together.
+  float ss[R], lg[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const int s = wave + W * j;
-    if (s >= n_sources) break;
-    float ss = 0.f, lg = 0.f;
+    ss[j] = 0.f;
     if constexpr (sizeof(T) == 2) {
       // bf16 bank: the same rounding points with the exact products and the fp32 sums on v_dot2c_f32_bf16
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
         if (on[c]) {
           const uint4 w = xr.x[j][c];
-          ss = dot2_bf16(w.x, w.x, dot2_bf16(w.y, w.y, dot2_bf16(w.z, w.z, dot2_bf16(w.w, w.w, ss))));
+          ss[j] = dot2_bf16(w.x, w.x, dot2_bf16(w.y, w.y, dot2_bf16(w.z, w.z, dot2_bf16(w.w, w.w, ss[j]))));
         }
-      const float r = rsqrtf(wave_sum(ss) * inv_dim + eps);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float x[8];
+        raw8<T>::unpack(xr.x[j][c], x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss[j] = fmaf(on[c] ? x[i] : 0.f, on[c] ? x[i] : 0.f, ss[j]);
+      }
+    }
+  }
+  wave_sums<R>(ss);
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const float r = rsqrtf(ss[j] * inv_dim + eps);
+    lg[j] = 0.f;
+    if constexpr (sizeof(T) == 2) {
+      // per piece in stages (the keys, the 8 products, their packing, the sums), so that independent
+      // instructions fill the wait states between a product and the conversion that reads it
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
         if (on[c]) {
           const uint4 w = xr.x[j][c];
           const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+          uint32_t k[4], pq[4];
+          float p[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            k[i] = pack_bf16x2(__uint_as_float(u[i] << 16) * r, __uint_as_float(u[i] & 0xffff0000u) * r);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const uint32_t k = pack_bf16x2(__uint_as_float(u[i] << 16) * r, __uint_as_float(u[i] & 0xffff0000u) * r);
-            const uint32_t pq = pack_bf16x2(dot2_bf16(k, qr.lo[c][i], 0.f), dot2_bf16(k, qr.hi[c][i], 0.f));
-            lg = dot2_bf16(pq, BF16_ONES, lg);
+            p[2 * i] = dot2_bf16(k[i], qr.lo[c][i], 0.f);
+            p[2 * i + 1] = dot2_bf16(k[i], qr.hi[c][i], 0.f);
           }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pq[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) lg[j] = dot2_bf16(pq[i], BF16_ONES, lg[j]);
         }
     } else {
-      float x[NCH][8];
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        raw8<T>::unpack(xr.x[j][c], x[c]);
+        float x[8];
+        raw8<T>::unpack(xr.x[j][c], x);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          if (!on[c]) x[c][i] = 0.f;
-          ss = fmaf(x[c][i], x[c][i], ss);
-        }
+        for (int i = 0; i < 8; ++i) lg[j] += (on[c] ? x[i] : 0.f) * r * qr.f[c][i];
       }
-      const float r = rsqrtf(wave_sum(ss) * inv_dim + eps);
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lg += x[c][i] * r * qr.f[c][i];
     }
-    lg = wave_sum(lg);
-    if (lane == 0) sm.logit[s] = lg;
   }
+  wave_sums<R>(lg);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (wave + W * j < n_sources && lane == 0) sm.logit[wave + W * j] = lg[j];
   __syncthreads();
   // softmax with one source per lane: e_s = exp(logit_s - max) in lane s, weight_s = e_s / sum e
   // (the cross-lane reductions run with every lane active)
@@ -323,7 +384,8 @@ __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const Quer
   for (int j = 0; j < R; ++j) {
     const int s = wave + W * j;
     if (s >= n_sources) break;
-    const float w = round_to_t<T>(__shfl(e_l, s) * inv_den);
+    // (s is wave-uniform: a lane read into a scalar register, no LDS round trip)
+    const float w = round_to_t<T>(__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e_l), s)) * inv_den);
     if constexpr (sizeof(T) == 2) {
       // round(x w): exact products on (w, 0) / (0, w) words; the fp32 sums on (1, 0) / (0, 1) words
       const uint32_t wl = __float_as_uint(w) >> 16, wh = __float_as_uint(w) & 0xffff0000u;
@@ -332,11 +394,19 @@ __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const Quer
       for (int c = 0; c < NCH; ++c) {
         const uint4 xw = xr.x[j][c];
         const uint32_t u[4] = {xw.x, xw.y, xw.z, xw.w};
+        float p[8];
+        uint32_t y[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t y = pack_bf16x2(dot2_bf16(u[i], wl, 0.f), dot2_bf16(u[i], wh, 0.f));
-          acc[c][2 * i] = dot2_bf16(y, one_lo, acc[c][2 * i]);
-          acc[c][2 * i + 1] = dot2_bf16(y, BF16_ONE_HI, acc[c][2 * i + 1]);
+          p[2 * i] = dot2_bf16(u[i], wl, 0.f);
+          p[2 * i + 1] = dot2_bf16(u[i], wh, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[c][2 * i] = dot2_bf16(y[i], one_lo, acc[c][2 * i]);
+          acc[c][2 * i + 1] = dot2_bf16(y[i], BF16_ONE_HI, acc[c][2 * i + 1]);
         }
       }
     } else {
@@ -371,7 +441,7 @@ __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const Quer
   }
 }
 
-template <typename T, int NCH, int R, int W>
+template <typename T, int NCH, int R, int W, bool FULL>
 __global__ __launch_bounds__(64 * W) void attnres_reg_kernel(const SourcePtrs src, int n_sources, int tokens,
                                                              int dim, long row_stride, const T* __restrict__ query,
                                                              float eps, T* __restrict__ out) {
@@ -396,7 +466,7 @@ __global__ __launch_bounds__(64 * W) void attnres_reg_kernel(const SourcePtrs sr
     }
   }
   const int t = blockIdx.x;
-  mix_token<T, NCH, R, W>(load_rowset<T, NCH, R, W>(src, n_sources, dim, row_stride, t, wave, lane), qr, sm,
+  mix_token<T, NCH, R, W, FULL>(load_rowset<T, NCH, R, W>(src, n_sources, dim, row_stride, t, wave, lane), qr, sm,
                           n_sources, dim, eps, t, wave, lane, out);
 }
 
@@ -408,11 +478,15 @@ void launch_attnres(const SourcePtrs& p, int n_sources, int tokens, int dim, lon
   const int r = (n_sources + W - 1) / W;     // rows per wave
   const int rr = r <= 4 ? r : r <= 6 ? 6 : 8;
   if (nch <= 2 && nch * rr * (int)sizeof(T) * 8 <= 256) {  // raw rows held per lane: at most 256 bytes
+    const bool full = dim == 512 * nch;
 #define ZGDN_ARR_CASE(N, RR)                                                                                    \
   if (nch == N && rr == RR) {                                                                                   \
-    hipLaunchKernelGGL((attnres_reg_kernel<T, N, RR, W>), dim3(tokens), dim3(64 * W), 0, stream, p, n_sources, \
-                       tokens,                                                                                 \
-                       dim, row_stride, (const T*)query, eps, (T*)out);                                        \
+    if (full)                                                                                                   \
+      hipLaunchKernelGGL((attnres_reg_kernel<T, N, RR, W, true>), dim3(tokens), dim3(64 * W), 0, stream, p,    \
+                         n_sources, tokens, dim, row_stride, (const T*)query, eps, (T*)out);                   \
+    else                                                                                                        \
+      hipLaunchKernelGGL((attnres_reg_kernel<T, N, RR, W, false>), dim3(tokens), dim3(64 * W), 0, stream, p,   \
+                         n_sources, tokens, dim, row_stride, (const T*)query, eps, (T*)out);                   \
     return;                                                                                                     \
   }
     ZGDN_ARR_CASE(1, 1) ZGDN_ARR_CASE(1, 2) ZGDN_ARR_CASE(1, 3) ZGDN_ARR_CASE(1, 4) ZGDN_ARR_CASE(1, 6)

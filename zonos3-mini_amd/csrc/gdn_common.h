@@ -78,22 +78,33 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Sum over all 64 lanes of a wave (result valid in every lane).
+// Sum over all 64 lanes of a wave (result valid in every lane): the row sums by DPP, then rows 0 + 1 and 2 + 3,
+// then the two halves, with the gfx950 permlane swaps (each lane gets its partner row's, then half's, value in
+// registers, no LDS round trip). The swaps pair lane l with l ^ 16, then l ^ 32, as lane-xor steps would, so
+// every lane's sum is the same to the bit.
 __device__ __forceinline__ float wave_sum(float x) {
   x = group_sum<16>(x);
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 // This wave's index in the workgroup as a wave-uniform (scalar) value: indexing by it then takes scalar
 // loads and branches (threadIdx.x >> 6 alone is a per-lane value to the compiler).
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// Maximum over all 64 lanes of a wave (result valid in every lane): DPP within each row of 16 lanes, then the
+// gfx950 permlane swaps (each lane gets its partner row's, then half's, value in registers).
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
+  x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_ROW_HALF_MIRROR>(x));
+  x = fmaxf(x, dpp<DPP_ROW_MIRROR>(x));
+  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
 // ---------------------------------------------------------------------------------------- packed sequences
