@@ -314,7 +314,7 @@ def bench_attnres(torch, gdn):
     return {"workload": "full_attnres_route: 23 sources x 4096 tokens x 1024, bf16 (the release LM's final mix)",
             "tokens_per_s": round(c["T"] / (k_ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "attnres_reg_kernel<bf16,2,6,4>",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "attnres_reg_kernel<bf16,2,6,4,full>",
                          "kernel_us": round(k_ms * 1e3, 3), "algorithmic_bytes": nbytes}}
 
 
