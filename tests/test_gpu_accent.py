@@ -1,6 +1,9 @@
 """Accent adapter shift kernel (zgdn_accent_shift, the drop-in for accent_shift / apply_accent of
 servers/sgl/src/zonos3_sgl/layers/accent.py:25-62 on the GDN mixer's in_proj and wo) against the oracle.
 
+Shapes cover both down kernels: the LDS-staged one (inputs of at most 1024, ranks up to 64, including a width
+that is not a multiple of 32) and the unstaged one (rank 256; 1040 inputs).
+
 Tolerances: float32 -> 1e-5 relative to the float64 statement; bfloat16 -> 2e-2 x max(1, max |ref|) max-abs to
 the torch restatement (both round x @ down.T, the masked product, the @ up product and the sum with y to
 bf16; they differ in summation order), i.e. within a couple of bf16 rounding steps. Batch invariance (the
@@ -48,7 +51,8 @@ def _check(got, x, down, up, mask, y, dtype):
 
 
 @pytest.mark.parametrize("rows,n_in,n_out,K", [(1, 1024, 2056, 64), (7, 1024, 2056, 16), (300, 512, 1024, 40),
-                                               (130, 1024, 2056, 256), (65, 64, 1032, 8)])
+                                               (130, 1024, 2056, 256), (65, 64, 1032, 8), (33, 1000, 520, 64),
+                                               (17, 1040, 264, 32)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_shift_against_the_oracle(gdn, cuda, rows, n_in, n_out, K, dtype):
     announce(f"accent shift rows={rows} in={n_in} out={n_out} K={K} {dtype}")

@@ -2,13 +2,15 @@
 // rounding points of the reference's bf16 torch ops (servers/sgl/src/zonos3_sgl/layers/accent.py:25-62:
 // x @ down.T rounded, times mask rounded, @ up rounded, added to y rounded).
 //
-// Two launches. accent_down_kernel forms tm = round(round(x . down^T) * mask) [rows, Kp] (Kp = K rounded up
-// to 32, zero columns past K) into a small workspace; accent_up_kernel streams y: each workgroup forms
+// Two launches. The down kernel (accent_down_lds_kernel, staged through LDS, for inputs of at most 1024 and
+// adapters of rank up to 64; accent_down_bf16_kernel otherwise) forms tm = round(round(x . down^T) * mask)
+// [rows, Kp] (Kp = K rounded up to 32, zero columns past K) into a small workspace; accent_up_kernel streams y: each workgroup forms
 // y_out = y_in + round(tm . up) for 64-row x 128-column blocks (y_out may be y_in), reading up in place. Both
 // run on bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation) for bf16; fp32 runs plain fp32 arithmetic.
 // Every row is computed on its own in a fixed order, so a row's result never depends on the other rows of
 // the call (the batch invariance the reference gets by padding to fixed-row blocks).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -125,6 +127,78 @@ __global__ __launch_bounds__(64 * down_waves<NT>()) void accent_down_bf16_kernel
   }
 }
 
+// The staged form of the same product, for inputs of at most 1024 and Kp <= 64 (the projections' 1024 and 512
+// inputs, adapters of rank up to 64): the block's 16 rows of x and down's Kp rows are read with coalesced
+// 16-byte loads (a wave reads 1 KiB of one row) into an LDS copy, 16-byte chunk c of row r at c ^ (r % 16), and
+// the MFMA fragments come from there. (Fragment loads straight from memory touch 16 rows 2 KiB apart per
+// instruction: measured 15.5 bytes per cycle per CU against 50-56 for coalesced reads of the same data.) Each
+// wave takes the same run of 32-input steps in the same MFMA order as accent_down_bf16_kernel and the partial
+// tiles are added in wave order, so the sums are the same; chunks past the input width are stored as zeros.
+constexpr int AC_LDS_CPR = 128;  // 16-byte chunks per staged row (in <= 1024)
+template <int NT>
+constexpr size_t down_lds_bytes() { return (size_t)(16 + 16 * NT) * AC_LDS_CPR * 16; }
+template <int NT>
+__global__ __launch_bounds__(1024) void accent_down_lds_kernel(const uint16_t* __restrict__ x, long x_ld,
+                                                               const uint16_t* __restrict__ down,
+                                                               const uint16_t* __restrict__ mask, long mask_ld,
+                                                               uint16_t* __restrict__ tm, int rows, int in, int K) {
+  constexpr int DW = 16, CPR = AC_LDS_CPR;
+  extern __shared__ uint4 lds4[];  // x [16][CPR], down [16 NT][CPR]; then the partial tiles [DW][NT][64]
+  const int Kp = kpad(K);
+  const int l = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
+  const int r0 = blockIdx.x * 16;
+  const int cpr = in / 8, steps = (in + 31) / 32, per = (steps + DW - 1) / DW;
+  const int s0 = wave * per, s1 = min(steps, s0 + per);
+  constexpr int FE = (16 * 16 * NT + 64 * DW - 1) / (64 * DW);  // output elements per thread, at most
+  uint16_t mk[FE];
+#pragma unroll
+  for (int j = 0; j < FE; ++j) {
+    const int e = tid + 64 * DW * j;
+    mk[j] = mask[(size_t)min(r0 + e / Kp, rows - 1) * mask_ld + min(e % Kp, K - 1)];
+  }
+  // every chunk of the staged rows: x's (rows past the batch re-read the last row, never stored) and down's
+  // (rows past K re-read row K - 1: their columns of tm are written as zeros)
+  constexpr int XJ = 16 * CPR / 1024, DJ = 16 * NT * CPR / 1024;
+#pragma unroll
+  for (int j = 0; j < XJ + DJ; ++j) {
+    const int e = tid + 1024 * (j < XJ ? j : j - XJ), row = e / CPR, ch = e % CPR;
+    const uint16_t* src = j < XJ ? x + (size_t)min(r0 + row, rows - 1) * x_ld : down + (size_t)min(row, K - 1) * in;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * min(ch, cpr - 1));
+    // (a select of whole uint4 values is compiled into a scratch array indexed by the condition: per word)
+    const uint32_t keep = ch < cpr ? ~0u : 0u;
+    lds4[(j < XJ ? row : 16 + row) * CPR + (ch ^ (row & 15))] =
+        make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+  }
+  __syncthreads();
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int m = l & 15, g = l >> 4;
+  for (int st = s0; st < s1; ++st) {
+    const int ch = 4 * st + g;
+    const bf16x8 a = __builtin_bit_cast(bf16x8, lds4[m * CPR + (ch ^ m)]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t] = mfma_bf16(a, __builtin_bit_cast(bf16x8, lds4[(16 + 16 * t + m) * CPR + (ch ^ m)]), acc[t]);
+  }
+  __syncthreads();  // the partial tiles overwrite the staged rows
+  f32x4* part = reinterpret_cast<f32x4*>(lds4);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) part[(wave * NT + t) * 64 + l] = acc[t];
+  __syncthreads();
+  // thread e finishes element (row e / Kp, column e % Kp) of the block, as accent_down_bf16_kernel does
+#pragma unroll
+  for (int j = 0; j < FE; ++j) {
+    const int e = tid + 64 * DW * j;
+    const int rl = e / Kp, k = e % Kp, r = r0 + rl, t = k >> 4, L = 16 * (rl >> 2) + (k & 15);
+    if (e >= 16 * Kp || r >= rows) break;
+    float sum = part[t * 64 + L][rl & 3];
+#pragma unroll
+    for (int w = 1; w < DW; ++w) sum += part[(w * NT + t) * 64 + L][rl & 3];
+    tm[(size_t)r * Kp + k] = k < K ? f32_to_bf16(rbf(sum) * bf16_to_f32(mk[j])) : (uint16_t)0;
+  }
+}
+
 typedef short short4_t __attribute__((ext_vector_type(4)));
 // Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes, lane s supplies the address of 4
 // consecutive 16-bit elements (row k0 + s/4, columns c0 + 4 (s%4) .. +3 of a row-major matrix) and lane i
@@ -175,7 +249,8 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
     uw[it] = *reinterpret_cast<const uint4*>(up + (size_t)min(k, K - 1) * out + min(n0 + c8, out - 8));
   }
   // then y_in of every block and the tm fragments of every block (wave w: rows 16 w .. +15 of each block, the
-  // MFMA N side)
+  // MFMA N side). (Staging tm through LDS with coalesced loads, as the down kernel does with its operands,
+  // measured slower here: 16 KiB a workgroup, against the extra LDS pass and barrier.)
   uint4 yw[AC_RB][PER];
   bf16x8 tb[AC_RB][KS];
 #pragma unroll
@@ -294,6 +369,24 @@ __global__ __launch_bounds__(256) void accent_up_f32_kernel(const float* __restr
   y_out[(size_t)r * y_out_ld + n] = (y_in != nullptr ? y_in[(size_t)r * y_in_ld + n] : 0.f) + acc;
 }
 
+// The staged down kernel's dynamic LDS (96 or 160 KiB) is above the default 64 KiB: raised once per device (the
+// first call on it); false when the device refuses, and the caller then takes the unstaged kernel.
+constexpr int AC_MAX_DEVICES = 64;
+template <int NT>
+bool down_lds_ready() {
+  static std::atomic<signed char> state[AC_MAX_DEVICES];  // 0 unknown, 1 ready, -1 refused
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= AC_MAX_DEVICES) return false;
+  const signed char st = state[dev].load(std::memory_order_acquire);
+  if (st != 0) return st > 0;
+  const bool ok = hipFuncSetAttribute((const void*)accent_down_lds_kernel<NT>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)down_lds_bytes<NT>()) == hipSuccess;
+  if (!ok) (void)hipGetLastError();  // (clear the refused call's error for the launches that follow)
+  state[dev].store(ok ? 1 : -1, std::memory_order_release);
+  return ok;
+}
+
 }  // namespace
 }  // namespace zgdn
 
@@ -339,10 +432,22 @@ extern "C" int zgdn_accent_shift(const void* x, long x_ld, const void* down, con
       hipLaunchKernelGGL(k1, g1, dim3(64 * down_waves<NT>()), 0, s, (const uint16_t*)x, x_ld, d, m, mask_ld, tm, rows,
                          in, K);
     };
-    if (Kp <= 32) go1(std::integral_constant<int, 2>{});
-    else if (Kp <= 64) go1(std::integral_constant<int, 4>{});
-    else if (Kp <= 128) go1(std::integral_constant<int, 8>{});
-    else go1(std::integral_constant<int, 16>{});
+    auto go_lds = [&](auto nt) -> bool {
+      constexpr int NT = decltype(nt)::value;
+      if (!down_lds_ready<NT>()) return false;
+      hipLaunchKernelGGL((accent_down_lds_kernel<NT>), g1, dim3(1024), down_lds_bytes<NT>(), s, (const uint16_t*)x,
+                         x_ld, d, m, mask_ld, tm, rows, in, K);
+      return true;
+    };
+    // the staged kernel where its LDS copy holds the rows (in <= 1024, Kp <= 64), else the unstaged one
+    const bool staged = in <= 8 * AC_LDS_CPR && Kp <= 64 &&
+                        (Kp <= 32 ? go_lds(std::integral_constant<int, 2>{}) : go_lds(std::integral_constant<int, 4>{}));
+    if (!staged) {
+      if (Kp <= 32) go1(std::integral_constant<int, 2>{});
+      else if (Kp <= 64) go1(std::integral_constant<int, 4>{});
+      else if (Kp <= 128) go1(std::integral_constant<int, 8>{});
+      else go1(std::integral_constant<int, 16>{});
+    }
     const bool aligned = (((uintptr_t)y_out | (uintptr_t)(y_in ? y_in : y_out)) % 16 == 0) && y_out_ld % 8 == 0 &&
                          (y_in == nullptr || y_in_ld % 8 == 0);
     const int n_nb = (out + AC_NB - 1) / AC_NB, n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
