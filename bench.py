@@ -504,7 +504,7 @@ def bench_accent(torch, reps=50):
             "speedup": round(timings["torch"] / timings["kernel"], 2),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
-                         "kernel": "accent_down_bf16_kernel<4> + accent_up_bf16_kernel<true,true>"}}
+                         "kernel": "accent_down_lds_kernel<4> + accent_up_bf16_kernel<true,true>"}}
 
 
 def calibrate_copy(torch):
