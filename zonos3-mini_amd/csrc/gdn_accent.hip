@@ -215,7 +215,7 @@ __device__ __forceinline__ uint2 lds_tr(const uint16_t* p) {
 // the output columns as the M side (A = up^T, read from the row-major tile with transposing LDS reads) and the
 // rows as the N side (B = tm rows), rounds them to bf16 through LDS in row order and adds them to its y
 // values: every y access is 16 contiguous bytes. KS: 32-wide adapter steps held (Kp <= 32 KS).
-constexpr int AC_RB = 2;  // 64-row blocks per phase-2 workgroup
+constexpr int AC_RB = 1;  // 64-row blocks per phase-2 workgroup (2 measured 1 us slower, 4 slower still)
 template <bool HAS_Y, bool ALIGNED, int KS>
 __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __restrict__ tm,
                                                              const uint16_t* __restrict__ up,
