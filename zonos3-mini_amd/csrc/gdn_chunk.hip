@@ -920,9 +920,20 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
 struct SegRun {
   int G, Cs;               // segments per sequence, chunks per segment (G == 1: plain runs)
   float* local_final;      // L [n_seqs * G][Hv][V][K]
-  float* trans_final;      // M^T [n_seqs * (G - 1)][Hv] as bf16 hi [K][K] then lo [K][K]
+  float* trans_final;      // M^T [n_seqs * (G - 1)][Hv] as bf16 hi then lo, each [K][K] in mt_frag order
   uint16_t* trans_out;     // Q' P^T [n_seqs * T][Hv][K] (bf16)
 };
+
+// Position (in 16-bit elements) of M^T[n][k] in the transition runs' stored maps: the order in which
+// chunk_combine_kernel's waves read them as MFMA B fragments -- fragment (w, t, kb) (columns n = 32 w + 16 t ..
+// + 15 of M, keys k = 32 kb ..) as 64 lanes x 8 elements, lane 16 ((k >> 3) & 3) + n % 16 holding keys
+// k & ~7 .. + 7 -- so that each fragment load is 1 KiB of contiguous memory. (Read as rows of M^T, a fragment
+// touched 16 rows per instruction, a third of the rate of contiguous reads.) Four consecutive keys k .. k + 3
+// (k % 4 == 0) are contiguous.
+__device__ __forceinline__ size_t mt_frag(int n, int k) {
+  const int w = n >> 5, t = (n >> 4) & 1, kb = k >> 5, g = (k >> 3) & 3;
+  return ((size_t)((w * 2 + t) * (DK / 32) + kb) * 64 + 16 * g + (n & 15)) * 8 + (k & 7);
+}
 
 template <typename TOut>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
@@ -997,7 +1008,7 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
 
   if (trans) {  // the segment map transposed (M^T[n][k] = M[k][n]), as bf16 hi and lo parts [K][K] each
     uint16_t* mt = reinterpret_cast<uint16_t*>(seg.trans_final + ((size_t)run * Hv + h) * hs);
-    const size_t off = (size_t)ncol * DK + vb * VB + 4 * (l >> 4);
+    const size_t off = mt_frag(ncol, vb * VB + 4 * (l >> 4));
     uint32_t h01, l01, h23, l23;
     split2(S[0], S[1], h01, l01);
     split2(S[2], S[3], h23, l23);
@@ -1281,11 +1292,12 @@ __global__ __launch_bounds__(256) void chunk_combine_kernel(const float* __restr
   };
   const bool want_final = s_out != nullptr;
   auto needed = [&](int g) { return g < G - 1 || (g == G - 1 && want_final); };  // step g's product
-  // B fragments of column tile t (M^T rows 32 wave + 16 t + l % 16) and key block k (32 k + 8 (l / 16) ..)
+  // B fragments of column tile t (M^T rows 32 wave + 16 t + l % 16) and key block k (32 k + 8 (l / 16) ..),
+  // stored in fragment order (mt_frag): 1 KiB of contiguous memory per load
   auto load_b = [&](const uint16_t* mt, int k, uint4* b) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const uint16_t* p = mt + (size_t)(32 * wave + 16 * t + (l & 15)) * DK + 32 * k + 8 * (l >> 4);
+      const uint16_t* p = mt + mt_frag(32 * wave + 16 * t + (l & 15), 32 * k + 8 * (l >> 4));
       b[(t * (DK / 32) + k) * 2] = *reinterpret_cast<const uint4*>(p);
       b[(t * (DK / 32) + k) * 2 + 1] = *reinterpret_cast<const uint4*>(p + hs);
     }
