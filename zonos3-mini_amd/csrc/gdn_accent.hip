@@ -216,6 +216,13 @@ __device__ __forceinline__ uint2 lds_tr(const uint16_t* p) {
 // rows as the N side (B = tm rows), rounds them to bf16 through LDS in row order and adds them to its y
 // values: every y access is 16 contiguous bytes. KS: 32-wide adapter steps held (Kp <= 32 KS).
 constexpr int AC_RB = 1;  // 64-row blocks per phase-2 workgroup (2 measured 1 us slower, 4 slower still)
+// Column blocks per row block: 128 columns each, a remainder of at most 8 columns folded into the last block
+// (which keeps those 8 columns of up and of its products in the 8 pad columns of its LDS rows). A 2056-column
+// projection then takes 16 blocks per row block instead of 17: 1024 workgroups for 4096 rows, one per slot at
+// four workgroups a CU, where the 17th block of 8 columns made a second round of 64 workgroups.
+__host__ __device__ inline int up_col_blocks(int out) {
+  return out > AC_NB && out % AC_NB <= 8 ? out / AC_NB : (out + AC_NB - 1) / AC_NB;
+}
 template <bool HAS_Y, bool ALIGNED, int KS>
 __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __restrict__ tm,
                                                              const uint16_t* __restrict__ up,
@@ -230,11 +237,12 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
   // Workgroup ids go round-robin over the 8 XCDs: all column blocks of one row block take ids of one residue
   // mod 8, so they run on one XCD and share its L2 copy of the 128-byte lines their rows straddle (the
   // projection's rows are rarely line-aligned: 2056 bf16 = 4112 bytes).
-  const int n_nb = (out + NB - 1) / NB, n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
+  const int n_nb = up_col_blocks(out), n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
   const int rblk = (slot / n_nb) * 8 + xcd, nblk = slot % n_nb;
   if (rblk >= n_rb) return;
   const int n0 = nblk * NB, rbase = rblk * (AC_ROWS * AC_RB);
+  const bool wide = nblk == n_nb - 1 && n0 + NB < out;  // the last block, with folded columns n0 + NB .. +7
   const int tid = threadIdx.x, l = tid & 63, wave = wave_id();
   constexpr int G = NB / 8;               // 16-byte groups per row of y
   constexpr int PER = AC_ROWS * G / 256;  // y groups per thread and block
@@ -248,39 +256,47 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
     const int e = tid + 256 * it, k = e / G, c8 = 8 * (e % G);
     uw[it] = *reinterpret_cast<const uint4*>(up + (size_t)min(k, K - 1) * out + min(n0 + c8, out - 8));
   }
-  // then y_in of every block and the tm fragments of every block (wave w: rows 16 w .. +15 of each block, the
-  // MFMA N side). (Staging tm through LDS with coalesced loads, as the down kernel does with its operands,
+  static_assert(AC_RB == 1, "the folded columns are handled for one row block a workgroup");
+  // the folded block's 8 extra columns of up (row tid), read by every workgroup from a clamped address so that
+  // no load sits under a condition (the others never store it)
+  const uint4 ux = *reinterpret_cast<const uint4*>(up + (size_t)min(tid, K - 1) * out + min(n0 + NB, out - 8));
+  // then the tm fragments of every block (wave w: rows 16 w .. +15 of each block, the MFMA N side) and, last,
+  // y_in of every block, so that the products' MFMA waits for the fragments only and the y loads stay in flight
+  // through it. (Staging tm through LDS with coalesced loads, as the down kernel does with its operands,
   // measured slower here: 16 KiB a workgroup, against the extra LDS pass and barrier.)
   uint4 yw[AC_RB][PER];
   bf16x8 tb[AC_RB][KS];
 #pragma unroll
   for (int b = 0; b < AC_RB; ++b) {
     const int r0 = rbase + AC_ROWS * b;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int e = tid + 256 * p, r = r0 + e / G, n = n0 + 8 * (e % G);
-      yw[b][p] = make_uint4(0, 0, 0, 0);
-      if constexpr (HAS_Y) {
-        const uint16_t* yp = y_in + (size_t)min(r, rows - 1) * y_in_ld + min(n, out - 8);
-        if constexpr (ALIGNED) {
-          yw[b][p] = *reinterpret_cast<const uint4*>(yp);
-        } else {
-          uint32_t u[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) u[j] = (uint32_t)yp[2 * j] | ((uint32_t)yp[2 * j + 1] << 16);
-          yw[b][p] = make_uint4(u[0], u[1], u[2], u[3]);
-        }
-      }
-    }
     const int rb = min(r0 + 16 * wave + (l & 15), rows - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) tb[b][ks] = load8(tm + (size_t)rb * Kp + min(32 * ks + 8 * (l >> 4), Kp - 8), true);
   }
+  auto load_y = [&](int r, int n) {
+    if constexpr (!HAS_Y) return make_uint4(0, 0, 0, 0);
+    const uint16_t* yp = y_in + (size_t)min(r, rows - 1) * y_in_ld + min(n, out - 8);
+    if constexpr (ALIGNED) return *reinterpret_cast<const uint4*>(yp);
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u[j] = (uint32_t)yp[2 * j] | ((uint32_t)yp[2 * j + 1] << 16);
+    return make_uint4(u[0], u[1], u[2], u[3]);
+  };
+#pragma unroll
+  for (int b = 0; b < AC_RB; ++b) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = tid + 256 * p;
+      yw[b][p] = load_y(rbase + AC_ROWS * b + e / G, n0 + 8 * (e % G));
+    }
+  }
+  const uint4 yx = load_y(rbase + (tid & (AC_ROWS - 1)), n0 + NB);  // the folded columns' y_in (row tid)
 #pragma unroll
   for (int it = 0; it < UPER; ++it) {
     const int e = tid + 256 * it, k = e / G, c8 = 8 * (e % G);
     if (k < Kp) *reinterpret_cast<uint4*>(&ut[k * SP + c8]) = k < K ? uw[it] : make_uint4(0, 0, 0, 0);
   }
+  if (wide && tid < Kp) *reinterpret_cast<uint4*>(&ut[tid * SP + NB]) = tid < K ? ux : make_uint4(0, 0, 0, 0);
   __syncthreads();
 
 #pragma unroll
@@ -311,13 +327,27 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
       *reinterpret_cast<uint2*>(&sh[rr * SP + c]) =
           make_uint2(pack_bf16x2(acc[t][0], acc[t][1]), pack_bf16x2(acc[t][2], acc[t][3]));
     }
-    __syncthreads();
+    // the folded columns as a ninth column tile whose last 8 columns repeat its first 8 (lanes with column
+    // offsets 8 .. 15 read 0 .. 7: every read stays inside the 8 pad columns of the row), those never stored
+    if (wide) {  // (after the other tiles are stored, in their registers)
+      f32x4 accx = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int e = tid + 256 * p, rl = e / G, cl = 8 * (e % G), r = r0 + rl, n = n0 + cl;
-      if (r >= rows || n >= out) continue;
+      for (int ks = 0; ks < KS; ++ks) {
+        if (32 * ks >= Kp) break;
+        const int k0 = 32 * ks + 8 * (l >> 4) + (sl >> 2);
+        const uint2 a0 = lds_tr(&ut[k0 * SP + NB + 4 * (sl & 1)]);
+        const uint2 a1 = lds_tr(&ut[(k0 + 4) * SP + NB + 4 * (sl & 1)]);
+        accx = mfma_bf16(__builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y)), tb[b][ks], accx);
+      }
+      if ((l >> 4) < 2)
+        *reinterpret_cast<uint2*>(&sh[rr * SP + NB + 4 * (l >> 4)]) =
+            make_uint2(pack_bf16x2(accx[0], accx[1]), pack_bf16x2(accx[2], accx[3]));
+    }
+    __syncthreads();
+    // y_out = y_in + products for 8 columns (local row rl, local column cl) of the block
+    auto finish = [&](int rl, int cl, const uint4& yv) {
       const uint4 sw = *reinterpret_cast<const uint4*>(&sh[rl * SP + cl]);
-      const uint32_t su[4] = {sw.x, sw.y, sw.z, sw.w}, yu[4] = {yw[b][p].x, yw[b][p].y, yw[b][p].z, yw[b][p].w};
+      const uint32_t su[4] = {sw.x, sw.y, sw.z, sw.w}, yu[4] = {yv.x, yv.y, yv.z, yv.w};
       uint32_t ou[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -325,7 +355,7 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
         const float y_lo = __uint_as_float(yu[j] << 16), y_hi = __uint_as_float(yu[j] & 0xffff0000u);
         ou[j] = HAS_Y ? pack_bf16x2(y_lo + s_lo, y_hi + s_hi) : su[j];
       }
-      uint16_t* op = y_out + (size_t)r * y_out_ld + n;
+      uint16_t* op = y_out + (size_t)(r0 + rl) * y_out_ld + n0 + cl;
       if constexpr (ALIGNED) {
         *reinterpret_cast<uint4*>(op) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
       } else {
@@ -335,7 +365,14 @@ __global__ __launch_bounds__(256) void accent_up_bf16_kernel(const uint16_t* __r
           op[2 * j + 1] = (uint16_t)(ou[j] >> 16);
         }
       }
+    };
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = tid + 256 * p, rl = e / G, cl = 8 * (e % G);
+      if (r0 + rl >= rows || n0 + cl >= out) continue;
+      finish(rl, cl, yw[b][p]);
     }
+    if (wide && tid < AC_ROWS && r0 + tid < rows) finish(tid, NB, yx);
     if (b + 1 < AC_RB) __syncthreads();  // the products' LDS is rewritten by the next block
   }
 }
@@ -450,7 +487,7 @@ extern "C" int zgdn_accent_shift(const void* x, long x_ld, const void* down, con
     }
     const bool aligned = (((uintptr_t)y_out | (uintptr_t)(y_in ? y_in : y_out)) % 16 == 0) && y_out_ld % 8 == 0 &&
                          (y_in == nullptr || y_in_ld % 8 == 0);
-    const int n_nb = (out + AC_NB - 1) / AC_NB, n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
+    const int n_nb = up_col_blocks(out), n_rb = (rows + AC_ROWS * AC_RB - 1) / (AC_ROWS * AC_RB);
     const dim3 g2(8 * n_nb * ((n_rb + 7) / 8));  // XCD-grouped ids (see the kernel)
     const size_t lds = ((size_t)Kp + AC_ROWS) * (AC_NB + 8) * 2;  // <= 87,040 bytes
     auto pick = [&](auto ks) -> void (*)(const uint16_t*, const uint16_t*, const uint16_t*, long, uint16_t*, long,
