@@ -745,9 +745,20 @@ __device__ __forceinline__ int load_flag(const int* f) {
   return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
+// accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. The state pass forms one
+// per chunk in scalar registers, so that its loads and stores take a fixed per-lane offset and no 64-bit vector
+// address arithmetic.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc raw_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Stores one O wave's outputs of chunk ci: rows t0 .. t0+3 (D layout) of value column vb * VB + j. Lanes l and
 // l ^ 1 (adjacent columns) swap two values by DPP so that each stores two rows as column pairs, 4-byte words
-// (8 for fp32) instead of 2-byte ones, with no per-row condition in full chunks.
+// (8 for fp32) instead of 2-byte ones. The stores go through a buffer resource covering the chunk's rows of
+// this job's columns up to the chunk's last token, so rows past the end of a partial chunk are dropped by the
+// range check instead of a per-row condition.
 template <typename TOut>
 __device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci, int t0, int j, const float* ov) {
   const bool odd = (lane_id() & 1) != 0;
@@ -755,18 +766,16 @@ __device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci
   // even lane (column j): rows t0, t0+1 as (own, partner); odd lane (column j): rows t0+2, t0+3 as (partner, own)
   const float a0 = odd ? r0 : ov[0], b0 = odd ? ov[2] : r0, a1 = odd ? r1 : ov[1], b1 = odd ? ov[3] : r1;
   const int tr = t0 + (odd ? 2 : 0), tlen = min(CH, a.len - ci * CH);
-  TOut* p = o + ((size_t)(a.bos + ci * CH + tr) * a.Hv + a.h) * DV + a.vb * VB + (j & ~1);
-  const size_t row = (size_t)a.Hv * DV;
-  auto pair = [](TOut* q, float u, float v) {
-    if constexpr (sizeof(TOut) == 2) *reinterpret_cast<uint32_t*>(q) = pack_bf16x2(u, v);
-    else *reinterpret_cast<float2*>(q) = make_float2(u, v);
-  };
-  if (tlen == CH) {
-    pair(p, a0, b0);
-    pair(p + row, a1, b1);
+  const uint32_t row = (uint32_t)a.Hv * DV * (uint32_t)sizeof(TOut);  // bytes from one token to the next
+  const Rsrc r = raw_rsrc(o + ((size_t)(a.bos + ci * CH) * a.Hv + a.h) * DV + a.vb * VB, (uint32_t)tlen * row);
+  const uint32_t off = (uint32_t)tr * row + (uint32_t)(j & ~1) * (uint32_t)sizeof(TOut);
+  if constexpr (sizeof(TOut) == 2) {
+    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(a0, b0), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(a1, b1), r, off + row, 0, 0);
   } else {
-    if (tr < tlen) pair(p, a0, b0);
-    if (tr + 1 < tlen) pair(p + row, a1, b1);
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a0), __float_as_uint(b0)}, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a1), __float_as_uint(b1)}, r, off + row, 0, 0);
   }
 }
 
@@ -782,30 +791,33 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   // position of key column 16 wave + l%16 in Ss, the inverse of kappa
   const int pcol = 32 * (wave >> 1) + 8 * ((l & 15) >> 2) + 4 * (wave & 1) + (l & 3);
 
-  auto chunk_ws = [&](int ci) { return a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK; };
-  // per-lane byte offsets inside a chunk's workspace (32-bit, so each load is a uniform base + lane offset)
+  // a chunk's workspace as a buffer resource (scalar registers, formed per chunk)
+  auto chunk_ws = [&](int ci) { return raw_rsrc(a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK, WS_CHUNK); };
+  // per-lane byte offsets inside a chunk's workspace, the same for every chunk
   const uint32_t offA = (uint32_t)(URole ? WS_WP : WS_QP) + (uint32_t)(tb * 4 * 64 + l) * 16u;
   const uint32_t offX = URole ? (uint32_t)WS_UB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 16u
                               : (uint32_t)WS_OB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 8u;
   const uint32_t offK = (uint32_t)WS_KT + (uint32_t)(wave * 2 * 64 + l) * 16u;
-  auto ld16 = [](const uint8_t* w, uint32_t off) { return *reinterpret_cast<const bf16x8*>(w + off); };
+  auto ld16 = [](Rsrc w, uint32_t off) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(w, off, 0, 0));
+  };
   // the next chunk's loads in groups spread over the phases of the current chunk
-  auto fetch1 = [&](const uint8_t* w, Pre& x) {
+  auto fetch1 = [&](Rsrc w, Pre& x) {
     x.A[0] = ld16(w, offA);
     x.A[1] = ld16(w, offA + 1024u);
-    x.GL = *reinterpret_cast<const float*>(w + WS_GL);
+    x.GL = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(w, 0, (int)WS_GL, 0));
   };
-  auto fetch2 = [&](const uint8_t* w, Pre& x) {
+  auto fetch2 = [&](Rsrc w, Pre& x) {
     x.A[2] = ld16(w, offA + 2048u);
     x.A[3] = ld16(w, offA + 3072u);
     if constexpr (URole) {
-      x.X = *reinterpret_cast<const uint4*>(w + offX);
+      x.X = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w, offX, 0, 0));
     } else {
-      const uint2 ob = *reinterpret_cast<const uint2*>(w + offX);
+      const uint2 ob = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(w, offX, 0, 0));
       x.X = make_uint4(ob.x, ob.y, 0, 0);
     }
   };
-  auto fetch3 = [&](const uint8_t* w, Pre& x) {
+  auto fetch3 = [&](Rsrc w, Pre& x) {
     x.KT[0] = ld16(w, offK);
     x.KT[1] = ld16(w, offK + 1024u);
   };
@@ -840,7 +852,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) sh.Ss[4 * (l >> 4) + i4][pcol] = f32_to_bf16(S[i4]);
     wait_ready(ni);
-    const uint8_t* wn = chunk_ws(ni);
+    const Rsrc wn = chunk_ws(ni);
     fetch1(wn, nxt);
     lds_barrier();
 
@@ -896,7 +908,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   {
     if constexpr (Wait) fl = load_flag(fbase);
     wait_ready(0);
-    const uint8_t* w0 = chunk_ws(0);
+    const Rsrc w0 = chunk_ws(0);
     fetch1(w0, b0);
     fetch2(w0, b0);
     fetch3(w0, b0);
