@@ -78,6 +78,34 @@ __device__ __forceinline__ void round2_t(float& a, float& b) {
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
+// The 8 rounded products of a piece: out[i] = (round(a[i].lo * lo[i].lo + a[i].hi * lo[i].hi),
+// round(a[i].lo * hi[i].lo + a[i].hi * hi[i].hi)) -- with one half of each lo / hi word zero, the exact products
+// of the pair's two halves, rounded to bf16 and packed. The products run on the three-operand v_dot2_f32_bf16
+// with an inline zero addend (the compiler forms dot2_bf16(a, b, 0.f) as v_dot2c_f32_bf16 on a register it
+// zeroes first, one more instruction per product). One block for all 12 instructions, so that a VALU read of a
+// dot product's result comes at least 3 instructions after it (the wait states it needs, which the compiler
+// does not know for an asm block's results): the first conversion reads products 6 and 7 instructions old,
+// the last 3 and 4.
+__device__ __forceinline__ void products8(const uint32_t (&a)[4], const uint32_t (&lo)[4], const uint32_t (&hi)[4],
+                                          uint32_t (&out)[4]) {
+  float t[8];
+  asm("v_dot2_f32_bf16 %4, %12, %16, 0\n\t"
+      "v_dot2_f32_bf16 %5, %12, %20, 0\n\t"
+      "v_dot2_f32_bf16 %6, %13, %17, 0\n\t"
+      "v_dot2_f32_bf16 %7, %13, %21, 0\n\t"
+      "v_dot2_f32_bf16 %8, %14, %18, 0\n\t"
+      "v_dot2_f32_bf16 %9, %14, %22, 0\n\t"
+      "v_dot2_f32_bf16 %10, %15, %19, 0\n\t"
+      "v_dot2_f32_bf16 %11, %15, %23, 0\n\t"
+      "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
+      "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
+      "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
+      "v_cvt_pk_bf16_f32 %3, %10, %11"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]),
+        "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(lo[0]), "v"(lo[1]), "v"(lo[2]), "v"(lo[3]), "v"(hi[0]),
+        "v"(hi[1]), "v"(hi[2]), "v"(hi[3]));
+}
 constexpr uint32_t BF16_ONE_HI = 0x3f800000u, BF16_ONES = 0x3f803f80u;
 // (1, 0): bf16 1.0 in the low half, in a register. As an immediate, the compiler encodes this operand as the
 // inline constant 1.0, which the instruction reads as the fp32 word 0x3f800000, i.e. (0, 1).
@@ -339,17 +367,10 @@ __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const Quer
           const uint4 w = xr.x[j][c];
           const uint32_t u[4] = {w.x, w.y, w.z, w.w};
           uint32_t k[4], pq[4];
-          float p[8];
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             k[i] = pack_bf16x2(__uint_as_float(u[i] << 16) * r, __uint_as_float(u[i] & 0xffff0000u) * r);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            p[2 * i] = dot2_bf16(k[i], qr.lo[c][i], 0.f);
-            p[2 * i + 1] = dot2_bf16(k[i], qr.hi[c][i], 0.f);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pq[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+          products8(k, qr.lo[c], qr.hi[c], pq);
 #pragma unroll
           for (int i = 0; i < 4; ++i) lg[j] = dot2_bf16(pq[i], BF16_ONES, lg[j]);
         }
@@ -394,15 +415,9 @@ __device__ __forceinline__ void mix_token(const RowSet<T, NCH, R> xr, const Quer
       for (int c = 0; c < NCH; ++c) {
         const uint4 xw = xr.x[j][c];
         const uint32_t u[4] = {xw.x, xw.y, xw.z, xw.w};
-        float p[8];
+        const uint32_t wlo[4] = {wl, wl, wl, wl}, whi[4] = {wh, wh, wh, wh};
         uint32_t y[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[2 * i] = dot2_bf16(u[i], wl, 0.f);
-          p[2 * i + 1] = dot2_bf16(u[i], wh, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) y[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+        products8(u, wlo, whi, y);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           acc[c][2 * i] = dot2_bf16(y[i], one_lo, acc[c][2 * i]);
