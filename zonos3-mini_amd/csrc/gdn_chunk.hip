@@ -56,7 +56,6 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
   lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 
-constexpr int LDQ = DK + 8;  // padded LDS row (bf16) of a 128-wide matrix
 constexpr int LDC = CH + 8;  // padded LDS row (bf16) of a 64-wide matrix
 constexpr int LDF = CH + 4;  // padded LDS row (fp32) of a 64-wide matrix
 
@@ -714,11 +713,15 @@ struct Pre {
 };
 
 // Single buffers suffice: each is rewritten only after a barrier that every reader of it has passed.
+// The state slice sits in 256-byte rows with 16-byte chunk c of row r at chunk c ^ r (r < 16): its fragment
+// reads (16 rows at one chunk) then meet every bank once. (With padded 272-byte rows each of those reads took
+// 8 LDS cycles, 4 of them bank conflicts, against 4 and none: measured with the hardware counters.)
 struct StateShared {
-  uint16_t Ss[VB][LDQ];   // state slice (bf16), key columns at positions pi(key): B operand of [W'; Q'] S^T
+  uint16_t Ss[VB * DK];   // state slice (bf16), key columns at positions pi(key): B operand of [W'; Q'] S^T
   uint16_t UhT[VB][LDC];  // U'^T, hi part   } A operands of the state update
   uint16_t UlT[VB][LDC];  // U'^T, lo part   }
 };
+__device__ __forceinline__ int ss_at(int r, int c) { return r * DK + ((((c >> 3) ^ r) & 15) << 3) + (c & 7); }
 
 struct StateArgs {
   const uint8_t* ws;
@@ -790,6 +793,17 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   const int t0 = 16 * tb + 4 * (l >> 4);  // first of this lane's 4 tokens (D layout rows)
   // position of key column 16 wave + l%16 in Ss, the inverse of kappa
   const int pcol = 32 * (wave >> 1) + 8 * ((l & 15) >> 2) + 4 * (wave & 1) + (l & 3);
+  // this lane's Ss addresses, the same for every chunk: its 4 state elements (rows 4 (l/16) + i4, column
+  // pcol) and its fragments (row l%16, columns 32 kk + 8 (l/16) ..)
+  // (the fragment addresses in 16-byte chunks, so that the compiler sees their alignment and keeps each read
+  // one 16-byte access)
+  int ss_w[4], ss_r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ss_w[i] = ss_at(4 * (l >> 4) + i, pcol);
+    ss_r[i] = ss_at(l & 15, 32 * i + 8 * (l >> 4)) >> 3;
+  }
+  const bf16x8* ss_chunks = reinterpret_cast<const bf16x8*>(sh.Ss);
 
   // a chunk's workspace as a buffer resource (scalar registers, formed per chunk)
   auto chunk_ws = [&](int ci) { return raw_rsrc(a.ws + ((size_t)(a.c0 + ci) * a.Hv + a.h) * WS_CHUNK, WS_CHUNK); };
@@ -850,7 +864,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
 
   auto process = [&](int ci, const Pre& cur, int ni, Pre& nxt) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[4 * (l >> 4) + i4][pcol] = f32_to_bf16(S[i4]);
+    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[ss_w[i4]] = f32_to_bf16(S[i4]);
     wait_ready(ni);
     const Rsrc wn = chunk_ws(ni);
     fetch1(wn, nxt);
@@ -860,8 +874,8 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     f32x4 x0 = zero4(), x1 = zero4();
 #pragma unroll
     for (int kk = 0; kk < 4; kk += 2) {
-      x0 = mfma(cur.A[kk], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk), x0);
-      x1 = mfma(cur.A[kk + 1], frag(&sh.Ss[0][0], LDQ, 0, 32 * kk + 32), x1);
+      x0 = mfma(cur.A[kk], ss_chunks[ss_r[kk]], x0);
+      x1 = mfma(cur.A[kk + 1], ss_chunks[ss_r[kk + 1]], x1);
     }
     const f32x4 x = x0 + x1;
     float ov[4];  // O role: this wave's outputs
