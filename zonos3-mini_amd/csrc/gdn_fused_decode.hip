@@ -57,7 +57,7 @@ struct FusedArgs {
   T* out;              // [B, Hv, V]
   const int64_t* slots;     // serving: rows of stream b; rows outside [0, n_rows) are skipped (else row b)
   long n_rows;
-  const int32_t* win_len;   // serving: real rows in each slot's window before this step
+  int32_t* win_len;         // serving: real rows in each slot's window, advanced by the step (see the kernel)
   T* conv_commit;           // serving: committed caches, written when the window fills
   float* state_commit;
   T* window;                // serving: [rows, window_rows, hidden] raw rows; receives stream b's row
@@ -68,6 +68,13 @@ struct FusedArgs {
   int qk_round;
 };
 
+// Channel of the group's i-th conv channel: q, k of key head hk, then the v of value heads hk*G ..
+__device__ __forceinline__ int conv_channel(int i, int hk, int Hk, int G) {
+  if (i < FD_K) return hk * FD_K + i;
+  if (i < 2 * FD_K) return Hk * FD_K + hk * FD_K + (i - FD_K);
+  return 2 * Hk * FD_K + hk * G * FD_K + (i - 2 * FD_K);
+}
+
 template <typename T, int G, int CW>
 __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const FusedArgs<T> p) {
   constexpr bool SERVING = CW == FD_W;  // slot-indexed caches, window and commits (the serving step)
@@ -77,6 +84,7 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
   __shared__ float s_o[G][FD_K];
   __shared__ float s_red[FD_WAVES][1];
   __shared__ float s_gate[G][2];
+  __shared__ int s_wlen;
 
   const int Hk = p.Hk, Hv = p.Hv;
   const int bs = blockIdx.x / Hk, hk = blockIdx.x % Hk;
@@ -90,13 +98,6 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane % FD_LPR, rsub = lane / FD_LPR;
   const int c0 = sub * 4, c1 = FD_K / 2 + sub * 4;
-  int wlen = 0;
-  bool commit = false;
-  if constexpr (SERVING) {
-    wlen = p.win_len[row];
-    commit = wlen + 1 == p.window_rows;
-  }
-
   // 0. issue the state loads of this lane's rows (row r = pass * 32 + wave * 4 + rsub; head r / 128)
   const size_t group_off = (row * Hv + (size_t)hk * G) * FD_K * FD_K;
   float* sgroup = p.state + group_off;
@@ -109,13 +110,18 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
     s[q][0] = u.x; s[q][1] = u.y; s[q][2] = u.z; s[q][3] = u.w;
     s[q][4] = w.x; s[q][5] = w.y; s[q][6] = w.z; s[q][7] = w.w;
   }
+  // The slot's window length, advanced in the same launch: workgroup hk of the slot adds 1 << 16 (an arrival
+  // count above the length, which stays below 2^16) and takes the length from the low bits of the old value;
+  // the last of the slot's Hk arrivals stores the new length (win_len + 1) % window_rows with the count
+  // cleared, so the word holds only the length once the launch ends. The atomic is issued here and its value
+  // is waited for only at the barrier that ends step 1.
+  int old_len = 0;
+  if (SERVING && tid == 0)
+    old_len = __hip_atomic_fetch_add(p.win_len + row, 1 << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // 1. conv + SiLU of the group's channels; the history rolls by one (the oldest input drops out)
   for (int i = tid; i < NCH; i += 64 * FD_WAVES) {
-    int ch;
-    if (i < FD_K) ch = hk * FD_K + i;                                     // q
-    else if (i < 2 * FD_K) ch = Hk * FD_K + hk * FD_K + (i - FD_K);       // k
-    else ch = 2 * Hk * FD_K + hk * G * FD_K + (i - 2 * FD_K);             // v of heads hk*G ..
+    const int ch = conv_channel(i, hk, Hk, G);
     const size_t hc = (row * C + ch) * CW;
     T* hist = p.conv_cache + hc + (CW - (FD_W - 1));  // the taps' history: the last W-1 columns
     const float xv = io<T>::load(p.x + bs * p.x_ld + ch);
@@ -131,25 +137,34 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
     io<T>::store(dst, h1);
     io<T>::store(dst + 1, h2);
     io<T>::store(dst + 2, xv);
-    if (SERVING && commit) {
-      T* cdst = p.conv_commit + hc;
-      if constexpr (CW == FD_W) io<T>::store(cdst++, h0);
-      io<T>::store(cdst, h1);
-      io<T>::store(cdst + 1, h2);
-      io<T>::store(cdst + 2, xv);
-    }
   }
   if (tid < G) {
     const int h = hk * G + tid;
     s_gate[tid][0] = __expf(-__expf(p.A_log[h]) * softplus(io<T>::load(p.a + bs * p.ab_ld + h) + p.dt_bias[h]));
     s_gate[tid][1] = sigmoid(io<T>::load(p.b + bs * p.ab_ld + h));
   }
-  if (SERVING && hk == 0 && wlen >= 0 && wlen < p.window_rows) {  // the raw row joins the slot's window
-    T* wrow = p.window + (row * p.window_rows + wlen) * p.hidden;
-    const T* xrow = p.x_hidden + (size_t)bs * p.hidden;
-    for (int i = tid; i < p.hidden; i += 64 * FD_WAVES) wrow[i] = xrow[i];
+  if (SERVING && tid == 0) {
+    s_wlen = old_len & 0xffff;
+    if ((old_len >> 16) == Hk - 1)
+      __hip_atomic_store(p.win_len + row, (s_wlen + 1) % p.window_rows, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  bool commit = false;
+  if constexpr (SERVING) {
+    const int wlen = s_wlen;
+    commit = wlen + 1 == p.window_rows;
+    if (hk == 0 && wlen < p.window_rows) {  // the raw row joins the slot's window
+      T* wrow = p.window + (row * p.window_rows + wlen) * p.hidden;
+      const T* xrow = p.x_hidden + (size_t)bs * p.hidden;
+      for (int i = tid; i < p.hidden; i += 64 * FD_WAVES) wrow[i] = xrow[i];
+    }
+    if (commit) {  // a full window commits the new conv history (this thread's own stores of step 1)
+      for (int i = tid; i < NCH; i += 64 * FD_WAVES) {
+        const size_t hc = (row * C + conv_channel(i, hk, Hk, G)) * CW;
+        for (int c = 0; c < CW; ++c) p.conv_commit[hc + c] = p.conv_cache[hc + c];
+      }
+    }
+  }
 
   // 2. L2 norms of q (wave 0) and k (wave 1): 2 values per lane
   if (wave < 2) {
@@ -223,16 +238,6 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
     const float nrm = round_to<T>(ov * rsqrtf(ms + p.eps) * io<T>::load(p.norm_w + j));
     const float zv = io<T>::load(p.z + bs * p.z_ld + (size_t)h * FD_K + j);
     io<T>::store(p.out + ((size_t)bs * Hv + h) * FD_K + j, nrm * silu(zv));
-  }
-}
-
-// Each listed slot's window gains the row just written: win_len = (win_len + 1) % window_rows.
-__global__ void advance_windows_kernel(const int64_t* __restrict__ slots, int32_t* __restrict__ win_len, int B,
-                                       long n_rows, int window_rows) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < B && slots[i] >= 0 && slots[i] < n_rows) {
-    int32_t* w = win_len + slots[i];
-    *w = (*w + 1) % window_rows;
   }
 }
 
@@ -361,11 +366,11 @@ extern "C" int zgdn_serving_decode_step(const void* mixed, long mixed_ld, const 
     p.qk_round = qk_round;
     launch_fused<T, FD_W>(G, B, p, s);
   };
+  if (window_rows >= (1 << 16))
+    return fail(ZGDN_EUNSUPPORTED, "%s: window_rows=%d (the step keeps the length below 2^16)", fn, window_rows);
   if (dtype == ZGDN_F32)
     fill((float*)nullptr);
   else
     fill((bf16*)nullptr);
-  hipLaunchKernelGGL(advance_windows_kernel, dim3((B + 255) / 256), dim3(256), 0, s, slots, win_len, B,
-                     (long)n_slots, window_rows);
   return check_launch(fn);
 }
