@@ -1,6 +1,6 @@
 """CPU restatement of ZONOS3-Mini's gated-DeltaNet (GDN) layer -- TEST INFRASTRUCTURE, not product code.
 
-Used only by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg, as the checker.
+Used only by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg, to check results.
 
 Two independent statements of the same mathematics live here:
 
