@@ -68,7 +68,7 @@ size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
  * Launch form of zgdn_chunk_fwd for this process: -1 the library's choice (above), 0 always phase 1 and the
  * state pass as two launches, 1 the overlapped launch for every eligible batch. The initial value is read once,
  * when the library is loaded, from the environment variable ZGDN_CHUNK_OVERLAP ("0" or "1"; otherwise -1); no
- * call reads the environment. This build's own control, with no counterpart in the reference (FLA picks its
+ * call reads the environment. The library's own control, with no counterpart in the reference (FLA picks its
  * launches itself). zgdn_chunk_get_launch_form returns the current value.
  */
 int zgdn_chunk_set_launch_form(int form);
