@@ -86,6 +86,26 @@ enum { ZGDN_STATUS_WAIT_GAVE_UP = 1 };
 int zgdn_chunk_status(int* status, int clear);
 
 /*
+ * The same status word without a synchronisation: enqueues on `stream` a copy of the current device's word into
+ * *host_status, which must be page-locked host memory (hipHostMalloc, torch's pin_memory=True); the value is
+ * there once the stream has passed the copy (an event recorded behind it tells). Does not clear the word. For
+ * callers that check their earlier launches from the host without stalling, as the serving layer does before
+ * its next call (the reference raises RuntimeError on what it can detect, servers/sgl/src/zonos3_sgl/models/
+ * gdn.py:241-272).
+ */
+int zgdn_chunk_status_async(int* host_status, void* stream);
+
+/*
+ * Queues of the overlapped launch for a device of n_cu compute units in n_xcc XCDs (accelerator complex dies,
+ * each with its own L2): one queue per XCD, the queue of a workgroup being its XCC_ID register modulo the
+ * count, so that a chunk's phase-1 producer and its state-pass consumers share one L2. Returns n_xcc when
+ * 1 <= n_xcc <= 8 and the CUs split evenly over the XCDs, else 0 (the overlapped launch is then not taken and
+ * zgdn_chunk_fwd runs its two launches). zgdn_chunk_fwd reads n_cu and n_xcc from the device
+ * (hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeNumberOfXccs). A host-only function.
+ */
+int zgdn_chunk_overlap_queues(int n_cu, int n_xcc);
+
+/*
  * Test control of the overlapped launch's waits for this process: `spins` bounds each wait (0 = the default,
  * about a few tenths of a second), and never_ready != 0 makes every wait treat its chunk as not ready, so that
  * each wait runs out after `spins` tries -- the way tests drive the error path of zgdn_chunk_status while
@@ -134,8 +154,11 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
 /*
  * zgdn_chunk_fwd without a workspace argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: FLA's
- * chunk_gated_delta_rule_fwd allocates its own intermediates. Same arguments, layouts and results as
- * zgdn_chunk_fwd (the same kernels); the caller still passes every input and output. The workspace is the
+ * chunk_gated_delta_rule_fwd allocates its own intermediates. Same arguments and layouts as zgdn_chunk_fwd,
+ * and the same results as zgdn_chunk_fwd given a workspace of the same size (the same kernels): the
+ * segmented state pass of long unpacked prompts is taken only when its extra space fits the scratch as well,
+ * else the plain pass, whose results differ from the segmented one's in the last bits (its combine rounds
+ * through bf16 hi / lo parts). The caller still passes every input and output. The workspace is the
  * library's own per-device scratch of zgdn_chunk_noalloc_max_bytes() bytes (64 MiB: 680 chunk x head items,
  * e.g. 4 heads up to 10,880 tokens or 16 heads up to 2,720), a static device array held by each device the
  * library runs on until the process ends; calls needing more fail with ZGDN_EINVAL before any launch. Its
@@ -178,8 +201,9 @@ int zgdn_fused_decode_step(const void* x_qkv, const void* z, const void* a, cons
  *   mixed [B, mixed_ld]: each request's in_proj row, q|k|v (C = 2 Hk K + Hv V) | z (Hv V) | a (Hv) | b (Hv)
  *   (the split of gdn.py:402), mixed_ld >= C + Hv V + 2 Hv; x_hidden [B, hidden]: the raw rows; out
  *   [B, Hv, V]; conv_weight [C, W]; norm_weight [V]: all of element type `dtype`.
- *   slots [B] int64, distinct: the requests' table slots (one outside [0, n_slots) is skipped: its caches
- *   are not touched and its out rows are left unwritten). Per slot (n_slots = cap): conv_live, conv_commit
+ *   slots [B] int64: the requests' table slots (one outside [0, n_slots) is skipped: its caches are not
+ *   touched and its out rows are left unwritten; a slot repeated later in the batch, as padded graph replays
+ *   repeat a spare slot, is served by its first entry only, the later entries' out rows left unwritten). Per slot (n_slots = cap): conv_live, conv_commit
  *   [cap, C, W] (the last W raw inputs, oldest first, `dtype`); state_live, state_commit [cap, Hv, V, K]
  *   float32; window [cap, window_rows, hidden] (`dtype`); win_len [cap] int32, the real rows in the window.
  *   Updates conv_live and state_live; writes the row into window[slot, win_len]; when the window fills

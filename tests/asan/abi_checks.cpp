@@ -79,6 +79,9 @@ int main() {
   expect("launch form", zgdn_chunk_set_launch_form(7), ZGDN_EINVAL, nullptr);
   expect("launch form default", zgdn_chunk_set_launch_form(-1), ZGDN_OK, nullptr);
   expect("chunk status null", zgdn_chunk_status(nullptr, 0), ZGDN_EINVAL, nullptr);
+  expect("chunk status async null", zgdn_chunk_status_async(nullptr, nullptr), ZGDN_EINVAL, nullptr);
+  expect("overlap queues 256/8", zgdn_chunk_overlap_queues(256, 8), 8, nullptr);
+  expect("overlap queues uneven", zgdn_chunk_overlap_queues(250, 8), 0, nullptr);
 
   // fused decode block, serving decode step
   expect("fused K", zgdn_fused_decode_step(p, p, p, p, 1, p, p, f, f, p, f, p, 4, 8, 16, 64, 64, 4, 1e-6f, 0.1f, 0,

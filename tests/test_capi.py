@@ -26,6 +26,7 @@ def test_header_declares_entry_points():
             "zgdn_gated_rmsnorm_fwd", "zgdn_serving_decode_step", "zgdn_attnres_route", "zgdn_accent_workspace_size",
             "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size", "zgdn_chunk_set_launch_form",
             "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit",
+            "zgdn_chunk_status_async", "zgdn_chunk_overlap_queues",
             "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc"} == _declared()
 
 
@@ -179,6 +180,23 @@ def test_launch_form_and_wait_limit_controls(gdn):
     assert lib.zgdn_chunk_set_wait_limit(-1, 0) == native.EINVAL
     assert lib.zgdn_chunk_set_wait_limit(0, 0) == native.OK
     assert lib.zgdn_chunk_status(None, 0) == native.EINVAL
+    assert lib.zgdn_chunk_status_async(None, None) == native.EINVAL
+
+
+def test_overlap_queue_mapping(gdn):
+    """The overlapped launch's queues: one per XCD when the CUs split evenly over 1 .. 8 XCDs (MI355X: 256 CUs,
+    8 XCDs), else 0 -- the two-launch form then runs (a host-only function, no GPU call)."""
+    from importlib import import_module
+
+    lib = import_module("zonos3-mini_amd._native").lib()
+    assert lib.zgdn_chunk_overlap_queues(256, 8) == 8
+    assert lib.zgdn_chunk_overlap_queues(32, 1) == 1    # one XCD of a partitioned device
+    assert lib.zgdn_chunk_overlap_queues(128, 4) == 4
+    assert lib.zgdn_chunk_overlap_queues(304, 8) == 8   # 38 CUs per XCD
+    assert lib.zgdn_chunk_overlap_queues(256, 0) == 0   # unknown XCD count
+    assert lib.zgdn_chunk_overlap_queues(256, 16) == 0  # more XCDs than the control block has queues
+    assert lib.zgdn_chunk_overlap_queues(250, 8) == 0   # CUs that do not split evenly
+    assert lib.zgdn_chunk_overlap_queues(4, 8) == 0
 
 
 def test_launch_form_reads_the_environment_once_at_load():

@@ -226,6 +226,59 @@ def test_static_decode_graph_replays_equal_eager_steps(serving, cuda):
             assert torch.equal(getattr(a.layer, name), getattr(b.layer, name)), (step, name)
 
 
+def test_padded_decode_with_a_repeated_spare_slot(serving, cuda):
+    """A padded decode batch that repeats one spare slot (as the engine pads graph replays with a dummy
+    request, servers/sgl/src/zonos3_sgl/engine/graph.py:147,195): the repeat is served once, so every slot's
+    live states, window and window length equal those of a batch naming each slot once, and the spare slot's
+    window length stays a length (below 64), step after step across a window fill."""
+    announce("serving mixer: padded decode batch [2, 0, 3, 3] vs [2, 0, 3, 5], 70 steps")
+    gen = torch.Generator().manual_seed(4471)
+    w = _weights(4470, torch.bfloat16)
+    a, b = _Driver(serving, w, cuda, capacity=6), _Driver(serving, w, cuda, capacity=6)
+    x0 = torch.randn(100, HIDDEN, generator=gen).to(torch.bfloat16).to(cuda)
+    for d in (a, b):
+        d.batch.reqs = d.batch.padded_reqs = d._advance([2, 0, 3], [50, 30, 20])
+        d.layer.forward(x0)
+    sa = torch.tensor([2, 0, 3, 3], dtype=torch.long, device=cuda)
+    sb = torch.tensor([2, 0, 3, 5], dtype=torch.long, device=cuda)
+    for step in range(70):
+        x = torch.randn(4, HIDDEN, generator=gen).to(torch.bfloat16).to(cuda)
+        ya = a.layer._decode_rows(x, sa, None)
+        yb = b.layer._decode_rows(x, sb, None)
+        torch.cuda.synchronize()
+        assert torch.equal(ya[:3], yb[:3]), step
+        for name in ("_live_state", "_live_conv", "_window", "_win_len", "_recurrent_state", "_conv_state"):
+            ta, tb = getattr(a.layer, name), getattr(b.layer, name)
+            assert torch.equal(ta[:5], tb[:5]), (step, name)
+        assert 0 <= int(a.layer._win_len[3]) < 64, (step, int(a.layer._win_len[3]))
+
+
+def test_device_error_surfaces_on_the_next_call(serving, gdn, cuda):
+    """A chunked launch whose bounded wait ran out (forced from the host: never-ready waits in the overlapped
+    launch) leaves that call's states undefined; the layer reads the device status word without a sync after
+    each eager prefill and raises RuntimeError on its next call, as the reference raises on what it detects
+    (gdn.py:241-272). The word is cleared by the raise."""
+    announce("serving mixer: a gave-up overlapped launch raises on the next call")
+    gen = torch.Generator().manual_seed(4481)
+    d = _Driver(serving, _weights(4480, torch.bfloat16), cuda, capacity=4)
+    assert gdn.ops.chunk_status() == 0
+    try:
+        gdn._native.call("zgdn_chunk_set_wait_limit", 4, 1)
+        with gdn.ops.launch_form(1):  # 2 requests x 4 heads = 8 chains: the overlapped launch
+            reqs = d._advance([0, 1], [300, 200])
+            d.batch.reqs = d.batch.padded_reqs = reqs
+            d.layer.forward(torch.randn(500, HIDDEN, generator=gen).to(torch.bfloat16).to(cuda))
+    finally:
+        gdn._native.call("zgdn_chunk_set_wait_limit", 0, 0)
+    torch.cuda.synchronize()
+    reqs = d._advance([0, 1], [1, 1])
+    d.batch.is_decode = True
+    d.batch.reqs = d.batch.padded_reqs = reqs
+    with pytest.raises(RuntimeError, match="gave up"):
+        d.layer.forward(torch.randn(2, HIDDEN, generator=gen).to(torch.bfloat16).to(cuda))
+    assert gdn.ops.chunk_status() == 0
+
+
 def test_in_place_route_equals_the_operator_seam(serving, cuda):
     """With the package's own five operators bound, ``_run_packed`` skips the seam's copies (slices of the
     projection and conv output read in place, sigmoid(b) in the chunked kernel): outputs and final states

@@ -93,6 +93,7 @@ def test_overlapped_wait_give_up_is_reported(gdn, cuda):
     x = {n: d[n].to(cuda) for n in ("q", "k", "v", "g", "beta")}
     gdn.ops.chunk_status(clear=True)
     lib = gdn._native.lib()
+    form0 = lib.zgdn_chunk_get_launch_form()  # the form at the start (ZGDN_CHUNK_OVERLAP may have set it)
     try:
         gdn._native.call("zgdn_chunk_set_wait_limit", 4, 1)
         with gdn.ops.launch_form(1):
@@ -108,7 +109,7 @@ def test_overlapped_wait_give_up_is_reported(gdn, cuda):
         o1, s1 = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
     with gdn.ops.launch_form(0):
         o0, s0 = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
-    assert lib.zgdn_chunk_get_launch_form() == -1
+    assert lib.zgdn_chunk_get_launch_form() == form0
     assert gdn.ops.chunk_status() == 0
     assert torch.equal(o1, o0) and torch.equal(s1, s0)
 

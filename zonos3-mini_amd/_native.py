@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "zgdn_chunk_set_launch_form": (c_int, [c_int]),
     "zgdn_chunk_get_launch_form": (c_int, []),
     "zgdn_chunk_status": (c_int, [POINTER(c_int), c_int]),
+    "zgdn_chunk_status_async": (c_int, [_P, _P]),
+    "zgdn_chunk_overlap_queues": (c_int, [c_int, c_int]),
     "zgdn_chunk_set_wait_limit": (c_int, [c_int, c_int]),
     "zgdn_chunk_segment_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "zgdn_chunk_fwd": (

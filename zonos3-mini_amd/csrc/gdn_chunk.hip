@@ -1539,6 +1539,21 @@ int device_cus() {
   return std::max(1, n_cu);
 }
 
+// Queues of the overlapped launch: one per XCD (their L2s are not coherent with each other), or 0 when the
+// device's shape does not allow the launch (an XCD count the control block has no room for, or CUs that do
+// not split evenly over the XCDs, so that the XCC_ID register would not name one queue per L2).
+int overlap_queues(int n_cu, int n_xcc) {
+  if (n_xcc < 1 || n_xcc > FQ_MAX || n_cu < n_xcc || n_cu % n_xcc != 0) return 0;
+  return n_xcc;
+}
+
+int device_xccs() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess)
+    return 0;
+  return n;
+}
+
 template <typename TG>
 void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const void* k, const void* v, const void* g,
                  const void* beta, const float* A_log, const float* dt_bias, const int32_t* cu,
@@ -1590,6 +1605,16 @@ extern "C" int zgdn_chunk_status(int* status, int clear) {
   if (e != hipSuccess) return zgdn::fail(ZGDN_EHIP, "zgdn_chunk_status: %s", hipGetErrorString(e));
   return ZGDN_OK;
 }
+
+extern "C" int zgdn_chunk_status_async(int* host_status, void* stream) {
+  if (host_status == nullptr) return zgdn::fail(ZGDN_EINVAL, "zgdn_chunk_status_async: null pointer");
+  const hipError_t e = hipMemcpyFromSymbolAsync(host_status, HIP_SYMBOL(zgdn::g_chunk_status), sizeof(int), 0,
+                                                hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e != hipSuccess) return zgdn::fail(ZGDN_EHIP, "zgdn_chunk_status_async: %s", hipGetErrorString(e));
+  return ZGDN_OK;
+}
+
+extern "C" int zgdn_chunk_overlap_queues(int n_cu, int n_xcc) { return zgdn::overlap_queues(n_cu, n_xcc); }
 
 extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
   const size_t items = (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0);
@@ -1665,12 +1690,12 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
   // phases 1 and 2 in one overlapped launch where it pays (overlap_wanted): unpacked batches of 8 .. 16 long
   // chains (few-chains order) on the plain pass, packed batches of up to 256 sequences and unpacked batches of more
   // chains (many-chains order)
-  const int n_q = std::min(FQ_MAX, std::max(1, device_cus() / 32));  // XCDs (32 CUs each on gfx950)
+  const int n_q = overlap_queues(device_cus(), device_xccs());  // one queue per XCD; 0: no overlapped launch
   const long n_chains = (long)N * Hv;
   const bool few = cu_seqlens == nullptr && n_chains <= (long)FQ_FEW_CHAINS * n_q;
-  const bool fits = few || ((cu_seqlens == nullptr || N <= FQ_MAX_SEQS) &&
-                            (n_chains + n_q - 1) / n_q <= FQ_MAX_QCHAINS);
-  if (!segmented && n_chunks > 0 && n_chains >= n_q && fits &&
+  const bool fits = n_q > 0 && (few || ((cu_seqlens == nullptr || N <= FQ_MAX_SEQS) &&
+                                         (n_chains + n_q - 1) / n_q <= FQ_MAX_QCHAINS));
+  if (!segmented && n_chunks > 0 && n_q > 0 && n_chains >= n_q && fits &&
       overlap_wanted(few, (long)n_chunks * Hv, (double)n_chunks / std::max(1, N), (n_chains + n_q - 1) / n_q)) {
     const int n_items = n_chunks * Hv;
     int* ctl_base = reinterpret_cast<int*>(ws + (size_t)n_items * WS_CHUNK);
@@ -1726,31 +1751,26 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
 
-// The scratch's device address on the current device (looked up on the first call per device); nullptr with a
-// recorded error on failure.
-void* scratch_on_current_device(const char* fn) {
+// The scratch's device address on the current device (looked up on the first call per device) into *out;
+// returns ZGDN_OK, or the status recorded with the error.
+int scratch_on_current_device(const char* fn, void** out) {
+  *out = nullptr;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) {
-    fail(ZGDN_EHIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
-    return nullptr;
-  }
-  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
-    fail(ZGDN_EUNSUPPORTED, "%s: device %d (supported: 0 .. %d)", fn, dev, NOALLOC_MAX_DEVICES - 1);
-    return nullptr;
-  }
+  if (e != hipSuccess) return fail(ZGDN_EHIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return fail(ZGDN_EUNSUPPORTED, "%s: device %d (supported: 0 .. %d)", fn, dev, NOALLOC_MAX_DEVICES - 1);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || ptr == nullptr) {
-      fail(ZGDN_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
-           e != hipSuccess ? hipGetErrorString(e) : "null address");
-      return nullptr;
-    }
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(ZGDN_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                  e != hipSuccess ? hipGetErrorString(e) : "null address");
     g_scratch_ptr[dev] = ptr;
   }
-  return g_scratch_ptr[dev];
+  *out = g_scratch_ptr[dev];
+  return ZGDN_OK;
 }
 }  // namespace
 }  // namespace zgdn
@@ -1785,8 +1805,9 @@ extern "C" int zgdn_chunk_fwd_noalloc(const void* q, const void* k, const void* 
     return fail(ZGDN_EINVAL, "%s: %d chunks x %d heads need %zu bytes of workspace, above the %zu-byte scratch "
                 "of this entry point (use zgdn_chunk_fwd with a caller workspace)", fn, nc, Hv, need,
                 NOALLOC_SCRATCH_BYTES);
-  void* ptr = scratch_on_current_device(fn);
-  if (ptr == nullptr) return ZGDN_EHIP;
+  void* ptr = nullptr;
+  const int st = scratch_on_current_device(fn, &ptr);
+  if (st != ZGDN_OK) return st;
   // the segmented state pass's extra space when it fits the scratch as well, else the plain pass
   size_t bytes = need;
   if (cu_seqlens == nullptr && B > 0 && T > 0) {

@@ -55,7 +55,8 @@ struct FusedArgs {
   const T* norm_w;
   float* state;        // [rows, Hv, V, K]
   T* out;              // [B, Hv, V]
-  const int64_t* slots;     // serving: rows of stream b; rows outside [0, n_rows) are skipped (else row b)
+  const int64_t* slots;     // serving: rows of stream b; rows outside [0, n_rows) are skipped (else row b), and
+                            // so is every stream whose slot an earlier stream of the batch already holds
   long n_rows;
   int32_t* win_len;         // serving: real rows in each slot's window, advanced by the step (see the kernel)
   T* conv_commit;           // serving: committed caches, written when the window fills
@@ -92,6 +93,12 @@ __global__ __launch_bounds__(64 * FD_WAVES) void fused_decode_kernel(const Fused
   if constexpr (SERVING) {
     srow = p.slots[bs];
     if (srow < 0 || srow >= p.n_rows) return;  // a slot outside the caches: nothing is read or written
+    // A slot named again later in the batch (padded graph replays repeat one spare slot) is served by its
+    // first stream only: the later ones read and write nothing, so every slot sees exactly Hk arrivals below
+    // and its window-length word keeps only the length.
+    int dup = 0;
+    for (int i = threadIdx.x; i < bs; i += blockDim.x) dup |= p.slots[i] == srow;
+    if (__syncthreads_or(dup)) return;
   }
   const size_t row = (size_t)srow;
   const int C = 2 * Hk * FD_K + Hv * FD_K;

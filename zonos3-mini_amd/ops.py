@@ -282,6 +282,34 @@ def check_chunk_status() -> None:
                            "phase-1 results; the outputs and final states of that call are undefined)")
 
 
+class StatusWatch:
+    """The chunked path's device status word read without stalling the host, for a caller that launches from
+    one stream again and again (the serving layer): ``arm()`` enqueues an asynchronous copy of the word into
+    page-locked host memory on the current stream, with an event behind it; ``check()`` looks at the last armed
+    copy only once its event has completed (a non-blocking query) and raises RuntimeError, clearing the word,
+    when a launch before it recorded an error. Neither call synchronises; both do nothing while the stream is
+    being captured into a graph."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.event = None
+
+    def arm(self) -> None:
+        if torch.cuda.is_current_stream_capturing():
+            return
+        _native.call("zgdn_chunk_status_async", self.host.data_ptr(), _stream(self.device))
+        self.event = torch.cuda.Event()
+        self.event.record(torch.cuda.current_stream(self.device))
+
+    def check(self) -> None:
+        if self.event is None or torch.cuda.is_current_stream_capturing() or not self.event.query():
+            return
+        self.event = None
+        if int(self.host[0]):
+            check_chunk_status()
+
+
 # Validation mode (ZGDN_VALIDATE=1 in the environment, read once at import): every chunk_fwd then synchronises
 # the device after its launch and raises RuntimeError when the device status word records an error. Off by
 # default, so that calls stay asynchronous and capturable.
@@ -420,7 +448,9 @@ def serving_decode_step(mixed, x_hidden, slots, conv_weight, conv_live, conv_com
     (the fast path of ``servers/sgl/src/zonos3_sgl/models/gdn.py:329-355``; C ABI ``zgdn_serving_decode_step``).
 
     mixed [B, >= C + Hv*128 + 2*Hv] in_proj rows (q|k|v | z | a | b, unit stride within a row); x_hidden
-    [B, hidden] the raw rows; slots int64 [B], distinct table slots. Caches over ``cap`` slots: conv_live,
+    [B, hidden] the raw rows; slots int64 [B], table slots (a slot repeated later in the batch -- the spare
+    slot of a padded graph replay -- is served by its first entry only; the later entries' rows of the result
+    are unspecified). Caches over ``cap`` slots: conv_live,
     conv_commit [cap, C, 4] and window [cap, R, hidden] in mixed's dtype; state_live, state_commit
     [cap, Hv, 128, 128] float32; win_len int32 [cap]. conv_weight [C, 4] or [C, 1, 4], norm_weight [128] in
     mixed's dtype; A_log, dt_bias float32 [Hv]. Returns the gated, normalised output [B, Hv, 128]."""

@@ -232,6 +232,7 @@ class OriginalGDN:
         self._static_mode = False
         self._graph_slots: Optional[torch.Tensor] = None
         self._static_rows: dict[int, torch.Tensor] = {}
+        self._status: Optional[ops.StatusWatch] = None
 
     # ------------------------------------------------------------------------------------------ caches
 
@@ -284,10 +285,25 @@ class OriginalGDN:
         self._static_mode = bool(enabled)
 
     def note_graph_forward(self, reqs) -> None:
-        """Host-side mirrors after a replayed decode step or prefill (gdn.py:228-233)."""
+        """Host-side mirrors after a replayed decode step or prefill (gdn.py:228-233); raises RuntimeError
+        when an earlier chunked launch of this layer recorded a device error, and arms the next check."""
+        self._status_check()
         for r in reqs:
             self._owners[r.table_idx] = (r.uid, r.is_cfg_uncond)
             self._lengths[r.table_idx] = r.device_len
+        self._status_arm()
+
+    def _status_check(self) -> None:
+        """RuntimeError when a chunked launch before the last armed status copy recorded an error (the
+        overlapped launch's bounded wait ran out: that call's states are undefined), read without a sync."""
+        if self._status is not None:
+            self._status.check()
+
+    def _status_arm(self) -> None:
+        if self._status is None and self._capacity and self._recurrent_state.is_cuda:
+            self._status = ops.StatusWatch(self._recurrent_state.device)
+        if self._status is not None:
+            self._status.arm()
 
     # ----------------------------------------------------------------------------------------- forward
 
@@ -309,6 +325,7 @@ class OriginalGDN:
             return self._forward_prefill_static(x, batch.gdn_prefill)
         if x.is_cuda and torch.cuda.is_current_stream_capturing():
             raise RuntimeError("GDN ragged path cannot be captured; graphs use the static window / prefill paths")
+        self._status_check()
         reqs = self._admit(batch, x.shape[0])
         mask = self._accent_mask()
         if mask is not None:  # a request's adapters: the mask row of its first new row
@@ -324,6 +341,8 @@ class OriginalGDN:
         for r in reqs:
             self._owners[r.slot] = r.owner
             self._lengths[r.slot] = r.end
+        if not batch.is_decode:
+            self._status_arm()
         return y
 
     def _admit(self, batch, rows: int) -> list[Request]:
