@@ -57,16 +57,15 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
  * Bytes of workspace zgdn_chunk_fwd needs for n_chunks 64-token chunks (over all sequences) and Hv value
  * heads: 98,560 bytes per chunk and head, then the control block of the overlapped launch (11,520 bytes and 4
  * per chunk and head, padded to 256). zgdn_chunk_fwd runs phase 1 (per chunk) and the sequential state pass
- * in one launch, side by side, where that measured faster than two launches: one sequence of 16 heads and
- * 4096 tokens and similar (8 .. 16 (sequence, head) chains of 64 chunks or more), and packed or batched
- * sequences with at least 3072 chunk x head items and 8 chunks or more per chain on average (up to 256 packed
- * sequences). zgdn_chunk_set_launch_form overrides that choice (the same results, bit for bit).
+ * as two launches; it can run them in one launch, side by side (the overlapped launch: unpacked batches, and
+ * packed batches of up to 256 sequences), which measured slower on every shape tried with the present phase 1
+ * and is taken only when zgdn_chunk_set_launch_form asks for it (the same results, bit for bit).
  */
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
 
 /*
- * Launch form of zgdn_chunk_fwd for this process: -1 the library's choice (above), 0 always phase 1 and the
- * state pass as two launches, 1 the overlapped launch for every eligible batch. The initial value is read once,
+ * Launch form of zgdn_chunk_fwd for this process: -1 the library's choice (two launches, above), 0 always
+ * phase 1 and the state pass as two launches, 1 the overlapped launch for every eligible batch. The initial value is read once,
  * when the library is loaded, from the environment variable ZGDN_CHUNK_OVERLAP ("0" or "1"; otherwise -1); no
  * call reads the environment. The library's own control, with no counterpart in the reference (FLA picks its
  * launches itself). zgdn_chunk_get_launch_form returns the current value.

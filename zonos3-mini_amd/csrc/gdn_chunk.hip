@@ -9,7 +9,7 @@
 //   U  = Ub - W S0^T                                                (the corrected values)
 //   O  = s diag(exp(G)) Q S0^T + P U  =  Q' S0^T + Ob,   Q' = s diag(exp(G)) Q - P W,   Ob = P Ub
 //   S  = exp(G_L) S0 + U'^T K,   U' = diag(exp(G_L - G)) U = Ub' - W' S0^T  (Ub', W' the rows of Ub, W scaled)
-// Phase 1 (chunk_prep_kernel, one workgroup per chunk x head, all independent) forms W', Q', K^T, Ub', Ob and
+// Phase 1 (chunk_prep_kernel, one item per chunk x head, all independent) forms W', Q', K^T, Ub', Ob and
 // G_L into a workspace. Phase 2 (chunk_state_kernel, one workgroup per sequence x head x 16 value rows) walks
 // the chunks in order keeping its 16 x 128 slice of the fp32 state in registers: one MFMA pass over [W'; Q']
 // gives U' and the outputs, a second the state update. Only the state pass is sequential, so the workspace is
@@ -92,24 +92,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
-// Tile (r0.., c0..) of A . B where A is row-major [.][lda] and B is given by its transpose Bt [.][ldb],
-// contraction over k in [0, kend) (kend a multiple of 32).
-__device__ __forceinline__ f32x4 tile_mm(const uint16_t* A, int lda, int r0, const uint16_t* Bt, int ldb, int c0,
-                                         int kend, f32x4 acc) {
-  for (int k0 = 0; k0 < kend; k0 += 32) acc = mfma(frag(A, lda, r0, k0), frag(Bt, ldb, c0, k0), acc);
-  return acc;
-}
-
-// 16x16x16 fp32 block product acc += A[16][16] . B[16][16] (row-major fp32 in LDS).
-__device__ __forceinline__ f32x4 mm16_f32(const float* A, int lda, const float* B, int ldb, f32x4 acc) {
-  const int l = lane_id();
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[(l & 15) * lda + 4 * s + (l >> 4)],
-                                                B[(4 * s + (l >> 4)) * ldb + (l & 15)], acc, 0, 0, 0);
-  return acc;
-}
-
 // Two D tiles (keys 32 kk + 0..15 and 32 kk + 16..31, one token column per lane) as one bf16 A fragment in
 // the kappa key order.
 __device__ __forceinline__ uint4 kappa_frag(f32x4 d0, f32x4 d1) {
@@ -149,6 +131,15 @@ __device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, cons
   return r;
 }
 
+// Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
+// accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. The state pass forms one
+// per chunk in scalar registers, so that its loads and stores take a fixed per-lane offset and no 64-bit vector
+// address arithmetic.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc raw_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // ----------------------------------------------------------------------------------------------- phase 1
 
 constexpr int P1_WAVES = 8;
@@ -156,151 +147,7 @@ constexpr int P1_THREADS = 64 * P1_WAVES;
 constexpr int P1_WGS_PER_CU = 2;
 constexpr int P1_WAVES_PER_SIMD = P1_WGS_PER_CU * P1_WAVES / 4;  // caps the registers per wave at 512 / 4
 
-// Phase-1 LDS matrices are unpadded and XOR-swizzled: 16-byte chunk c of row r is stored at chunk
-// c ^ swz(r), which keeps the 16-row fragment reads and the D-layout writes free of bank conflicts without
-// padding, so that two workgroups fit on a CU. 256-byte rows (CPR = 16 chunks per row) swizzle with r % 16,
-// 128-byte rows (CPR = 8) with (r / 2) % 8.
-template <int CPR>
-__device__ __forceinline__ int swz(int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); }
-// element offset of (row, column): 16-bit elements (8 per chunk) and 32-bit elements (4 per chunk)
-template <int CPR>
-__device__ __forceinline__ int at16(int r, int c) { return r * (CPR * 8) + (((c >> 3) ^ swz<CPR>(r)) << 3) + (c & 7); }
-template <int CPR>
-__device__ __forceinline__ int at32(int r, int c) { return r * (CPR * 4) + (((c >> 2) ^ swz<CPR>(r)) << 2) + (c & 3); }
-
-// Per-lane parts of the swizzled fragment addresses, formed once per item. A fragment's rows r0 .. r0 + 15
-// start at a multiple of 16, so the swizzle of row r0 + lane%16 depends on the lane only and a fragment
-// address is the row-tile base plus one of these offsets (in elements).
-struct SwLane {
-  int row8, row16;  // (lane % 16) * row length, 128-byte and 256-byte rows
-  int k8[2];        // chunk offsets of k-steps 0, 1 (32 columns each) in 128-byte rows
-  int k16[4];       // chunk offsets of k-steps 0..3 in 256-byte rows
-  __device__ __forceinline__ explicit SwLane(int l) {
-    const int m = l & 15, g = l >> 4;
-    row8 = m * 64;
-    row16 = m * 128;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) k8[kk] = ((4 * kk + g) ^ (m >> 1)) << 3;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) k16[kk] = ((4 * kk + g) ^ m) << 3;
-  }
-};
-
-// MFMA A / B fragment (rows r0 + lane%16, columns 32 kk + 8*(lane/16) .. +7) of a swizzled bf16 matrix.
-template <int CPR>
-__device__ __forceinline__ bf16x8 sfrag(const uint16_t* m, int r0, int kk, const SwLane& sw) {
-  const int off = CPR == 16 ? r0 * 128 + sw.row16 + sw.k16[kk] : r0 * 64 + sw.row8 + sw.k8[kk];
-  return *reinterpret_cast<const bf16x8*>(m + off);
-}
-
-// Tile (r0.., c0..) of A . B for swizzled A (row-major) and Bt (B transposed), contraction over [0, kend).
-template <int CPRA, int CPRB>
-__device__ __forceinline__ f32x4 stile(const uint16_t* A, int r0, const uint16_t* Bt, int c0, int kend,
-                                       const SwLane& sw, f32x4 acc) {
-#pragma unroll
-  for (int kk = 0; kk < (CPRA == 16 ? 4 : 2); ++kk)
-    if (32 * kk < kend) acc = mfma(sfrag<CPRA>(A, r0, kk, sw), sfrag<CPRB>(Bt, c0, kk, sw), acc);
-  return acc;
-}
-
-// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes, lane s supplies the address of 4
-// consecutive bf16 (row k0 + s/4, columns c0 + 4 (s%4) .. +3 of a row-major matrix) and lane i receives column
-// c0 + i of rows k0 .. k0 + 3.
 typedef short short4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ short4_t lds_read_tr(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
-}
-
-// MFMA A / B fragment of M^T (rows r0 + lane%16 of M^T = columns of M, k = 32 kk + 8 (lane/16) .. +7 = rows of
-// M) from the row-major swizzled [64][128] bf16 matrix M: two transposing reads of 4 rows each.
-__device__ __forceinline__ bf16x8 tfrag(const uint16_t* M, int r0, int kk) {
-  const int l = lane_id(), s = l & 15;
-  const int k0 = 32 * kk + 8 * (l >> 4) + (s >> 2), c = r0 + 4 * (s & 3);
-  const short4_t lo = lds_read_tr(M + at16<16>(k0, c)), hi = lds_read_tr(M + at16<16>(k0 + 4, c));
-  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
-  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
-}
-
-// Tile (r0.., c0..) of A . B with A = M^T read transposed from the row-major M (keys x tokens, contraction over
-// tokens [0, kend)) and B given by the swizzled 128-byte-row Bt.
-__device__ __forceinline__ f32x4 stile_ta(const uint16_t* M, int r0, const uint16_t* Bt, int c0, int kend,
-                                          const SwLane& sw, f32x4 acc) {
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-    if (32 * kk < kend) acc = mfma(tfrag(M, r0, kk), sfrag<8>(Bt, c0, kk, sw), acc);
-  return acc;
-}
-
-// Tile (r0.., c0..) of A . B with A the swizzled 128-byte-row matrix and B = M read transposed from the
-// row-major M (tokens x values, contraction over tokens [0, kend)).
-__device__ __forceinline__ f32x4 stile_tb(const uint16_t* A, int r0, const uint16_t* M, int c0, int kend,
-                                          const SwLane& sw, f32x4 acc) {
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-    if (32 * kk < kend) acc = mfma(sfrag<8>(A, r0, kk, sw), tfrag(M, c0, kk), acc);
-  return acc;
-}
-
-// 16x16x16 fp32 block product acc += A[ra.., ca..] . B[rb.., cb..] of swizzled 64x64 fp32 matrices.
-__device__ __forceinline__ f32x4 mm16_f32(const float* A, int ra, int ca, const float* B, int rb, int cb, int l,
-                                          f32x4 acc) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[at32<16>(ra + (l & 15), ca + 4 * s + (l >> 4))],
-                                                B[at32<16>(rb + 4 * s + (l >> 4), cb + (l & 15))], acc, 0, 0, 0);
-  return acc;
-}
-
-// acc += (A1 - A2)[ra.., ca..] . B[rb.., cb..] (16x16 blocks of swizzled 64x64 fp32 matrices; A2's block at
-// ra2, ca2).
-__device__ __forceinline__ f32x4 mm16_f32_diff(const float* A1, int ra, int ca, const float* A2, int ra2, int ca2,
-                                               const float* B, int rb, int cb, int l, f32x4 acc) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const float a = A1[at32<16>(ra + (l & 15), ca + 4 * s + (l >> 4))] - A2[at32<16>(ra2 + (l & 15), ca2 + 4 * s + (l >> 4))];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, B[at32<16>(rb + 4 * s + (l >> 4), cb + (l & 15))], acc, 0, 0, 0);
-  }
-  return acc;
-}
-
-// A 16x16 D tile (rows r0 + 4 (lane / 16) + i, column c0 + lane % 16) into a swizzled 64x64 fp32 matrix,
-// negated when asked.
-__device__ __forceinline__ void put16_f32(float* M, int r0, int c0, int l, f32x4 d, bool neg) {
-#pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) M[at32<16>(r0 + 4 * (l >> 4) + i4, c0 + (l & 15))] = neg ? -d[i4] : d[i4];
-}
-
-struct Prep {
-  // one 32 KiB region reused by phase: raw q rows -> A, T (fp32) -> the bf16 forms of T and R -> Ub^T
-  union {
-    struct {
-      uint16_t Qs[CH * DK];  // raw q rows, 256-byte rows (A operand of Q K^T)
-    } a;
-    struct {
-      float As[CH * CH];  // strictly lower A (fp32, 256-byte rows), then N_ij = T_ii A_ij in its blocks
-      float Ts[CH * CH];  // T = (I + A)^-1 (fp32); blocks (0, 1..3) hold the inverse's pair products
-    } b;
-    struct {
-      uint16_t TBF[CH * CH];  // diag(Fk) T diag(beta exp(G) rk)   (B operand of W'^T)
-      uint16_t TBT[CH * CH];  // (T diag(beta exp(G) rk))^T         (B operand of R)
-      uint16_t LB[CH * CH];   // (T - I) diag(beta)                 (A operand of Ub)
-      uint16_t Rs[CH * CH];   // R = P T diag(beta exp(G) rk), so that P W = R K (B operand of Q'^T)
-    } c;
-    uint16_t UbT[DV * CH];  // Ub^T (B operand of Ob = P Ub), over TBF and TBT once W' and R are formed
-  } u;
-  uint16_t Ks[CH * DK];  // raw k rows: both operands of K K^T, the B operand of Q K^T; read transposed as the A
-                         // operand of W'^T and Q'^T and for the K^T fragments
-  uint16_t Vs[CH * DV];  // v rows, read transposed as the B operand of Ub and for the exact diagonal term
-  uint16_t Ps[CH * CH];   // P (bf16, zero above the diagonal blocks)
-  float Gs[CH];
-  float Bs[CH];
-  float Rk[CH];  // per-token L2 factor of k (1 without the fused norm)
-  float Ai[CH];  // beta rk: row factor of A
-  float Pi[CH];  // s rq: row factor of P
-  float Bk[CH];  // beta exp(G) rk
-  float Fq[CH];  // s exp(G) rq
-  float Fk[CH];  // exp(G_L - G) rk
-};
 
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -314,16 +161,6 @@ __device__ __forceinline__ void lower_tile(int t, int& rb, int& cb) {
   cb = t - rb * (rb + 1) / 2;
 }
 
-// Zero the 6 blocks above the diagonal of a swizzled 64x64 bf16 matrix with 16x16 blocks.
-__device__ __forceinline__ void zero_upper_blocks(uint16_t* m) {
-  for (int e = threadIdx.x; e < 6 * 256; e += P1_THREADS) {
-    const int t = e / 256, w = e % 256;
-    const int rb = t < 3 ? 0 : (t < 5 ? 1 : 2);
-    const int cb = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    m[at16<8>(rb * 16 + w / 16, cb * 16 + w % 16)] = 0;
-  }
-}
-
 // Contraction length over tokens for token tile tb of a lower-triangular left operand.
 __device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
 
@@ -335,354 +172,576 @@ struct RowStrides {
   int beta_sigmoid;
 };
 
-// One phase-1 item (chunk x head, item = chunk * Hv + head): W', Q', K^T, Ub', Ob and G_L of the chunk into its
-// workspace. Ends with a workgroup barrier (the LDS may be reused at once).
-template <typename TG, bool GATE>
-__device__ __forceinline__ void prep_item(Prep& sm, int item,
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
-    int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
-    uint8_t* __restrict__ ws) {
-  const int wave = threadIdx.x >> 6;
-  {
-    // thread indices made opaque per item: the swizzled LDS addresses derived from them are then formed
-    // where they are used instead of being hoisted out of the loop and kept live (or spilled) throughout
-    int tz = 0;
-    asm volatile("" : "+v"(tz));
-    const int tid = (int)threadIdx.x + tz, l = tid & 63;
-    // step 1: 16 lanes read one whole 256-byte row (8 full cache lines per load instruction); thread (rr, cg)
-    // holds columns c8 .. c8+7 of rows rr and rr + 32
-    const int rr = tid >> 4, c8 = (tid & 15) * 8;
-    const int r0 = rr, r1 = rr + CH / 2;
-    const SwLane sw(l);
-    const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
-    const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
-    uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
+// ----------------------------------------------------------------------------------------------- phase 1
+//
+// One item = one (chunk, value head): W', Q', K^T, Ub', Ob and G_L of the chunk into its workspace. Persistent
+// workgroups of 8 waves, two per CU (75,776 bytes of LDS each), loop over items. The item is laid out for few
+// VALU instructions and a short dependent chain:
+// * every LDS access is a per-lane offset formed once plus a compile-time or wave-uniform part: the XOR
+//   swizzles (16-byte chunk c of row r at c ^ (r % 16) for 256-byte rows, c ^ ((r / 2) % 8) for 128-byte rows,
+//   which keeps 16-row fragment reads free of bank conflicts without padding) are arranged so that a tile's or
+//   k-step's part is one XOR or an immediate on the lane's offset;
+// * a D tile is stored transposed (row n of X^T holds the tile's 4 rows of column n: one 16-byte fp32 or 8-byte
+//   bf16 write a lane), and its consumers read X's row fragments with transposing reads (ds_read_b64_tr_b16:
+//   within 16 lanes, lane s names row k0 + s/4, columns c0 + 4 (s%4) .. + 3, and lane i receives column c0 + i
+//   of the 4 rows) or take X^T's rows: A^T, P^T, T^T, (diag(Fk) T diag(Bk))^T, ((T - I) diag(beta))^T, R^T, Ub^T;
+// * the rows are read with buffer loads (a scalar base per item; rows past the chunk end fall outside the
+//   buffer range and read zero), the next item's rows in flight while the current item computes;
+// * the diagonal 16x16 blocks of T = (I + A)^-1 are inverted by one wave by right-looking substitution from rows
+//   of A^T (column c of a block per lane: once t_m is final every later row's partial sum takes one FMA, so the
+//   dependent chain is one FMA a row, not a row's dot product) while the other waves scale and store the other
+//   tiles; the off-diagonal blocks follow in three levels of 16x16 fp32 block products:
+//   N_ij = T_ii A_ij; T_10, T_21, T_32 = -N_10 T_00, -N_21 T_11, -N_32 T_22 and the pair products N_21 N_10,
+//   N_32 N_20, N_32 N_21; then T_20 = (N_21 N_10 - N_20) T_00, T_31 = (N_32 N_21 - N_31) T_11 and
+//   T_30 = (N_32 N_20 - N_30) T_00 + (N_32 N_21 - N_31) T_10;
+// * barriers wait for LDS traffic only: the workspace stores and the next item's loads stay in flight.
+// (An earlier form of this item recomputed its swizzled addresses per element and took the diagonal blocks by
+// a row-by-row dot-product substitution: 10.1-10.9k VALU instructions an item against 5.3k, 38.5 against
+// 30.7 us for the 1,024 items of a 4096-token, 16-head prefill.)
 
-    // gate inputs of the chunk's tokens (wave 7), loaded first so that their latency overlaps the rows'
-    float gi = 0.f, bi = 0.f, alog = 0.f, dtb = 0.f;
-    if (wave == P1_WAVES - 1 && l < cr.len) {
-      const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
-      gi = io<TG>::load(g + gh);
-      bi = io<TG>::load(beta + gh);
-      if constexpr (GATE) {
-        alog = A_log[h];
-        dtb = dt_bias[h];
-      }
-    }
+// byte offsets in the item's LDS block
+constexpr int PS_Q = 0;            // raw q rows [64][128] bf16 (256-byte rows)        } one 32 KiB region,
+constexpr int PS_AT = 0;           // A^T, then N^T in its blocks, fp32 [64][64]        } reused by phase
+constexpr int PS_TT = 16384;       // T^T fp32 (logical blocks (0, 1..3): pair products)
+constexpr int PS_TBF = 0;          // (diag(Fk) T diag(Bk))^T bf16 [64][64] (128-byte rows)
+constexpr int PS_TBT = 8192;       // (T diag(Bk))^T
+constexpr int PS_LB = 16384;       // ((T - I) diag(beta))^T
+constexpr int PS_RT = 24576;       // R^T
+constexpr int PS_UBT = 0;          // Ub^T bf16 [128][64]
+constexpr int PS_K = 32768;        // k rows [64][128] bf16
+constexpr int PS_V = 49152;        // v rows
+constexpr int PS_PT = 65536;       // P^T bf16 [64][64]; the blocks of zeros above P's diagonal blocks set once
+constexpr int PS_F = 73728;        // per-token factors: 8 x 64 floats
+constexpr int PSF_G = 0, PSF_B = 256, PSF_RK = 512, PSF_AI = 768, PSF_PI = 1024, PSF_BK = 1280, PSF_FQ = 1536,
+              PSF_FK = 1792;
+constexpr int PS_BYTES = PS_F + 2048;  // 75,776
+struct alignas(16) PrepShared {
+  uint8_t b[PS_BYTES];
+};
 
-    // 1. rows of q, k, v -> LDS (zeros past the chunk end), row-major; gate and G.
-    {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      uint4 q0 = z, q1 = z, k0 = z, k1 = z, v0 = z, v1 = z;
-      if (r0 < cr.len) {
-        const size_t t = (size_t)(cr.t0 + r0);
-        q0 = *reinterpret_cast<const uint4*>(q + t * rs.q + hk * DK + c8);
-        k0 = *reinterpret_cast<const uint4*>(k + t * rs.k + hk * DK + c8);
-        v0 = *reinterpret_cast<const uint4*>(v + t * rs.v + h * DV + c8);
-      }
-      if (r1 < cr.len) {
-        const size_t t = (size_t)(cr.t0 + r1);
-        q1 = *reinterpret_cast<const uint4*>(q + t * rs.q + hk * DK + c8);
-        k1 = *reinterpret_cast<const uint4*>(k + t * rs.k + hk * DK + c8);
-        v1 = *reinterpret_cast<const uint4*>(v + t * rs.v + h * DV + c8);
-      }
-      *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r0, c8)]) = q0;
-      *reinterpret_cast<uint4*>(&sm.u.a.Qs[at16<16>(r1, c8)]) = q1;
-      *reinterpret_cast<uint4*>(&sm.Ks[at16<16>(r0, c8)]) = k0;
-      *reinterpret_cast<uint4*>(&sm.Ks[at16<16>(r1, c8)]) = k1;
-      *reinterpret_cast<uint4*>(&sm.Vs[at16<16>(r0, c8)]) = v0;
-      *reinterpret_cast<uint4*>(&sm.Vs[at16<16>(r1, c8)]) = v1;
-    }
-    if (wave == P1_WAVES - 1) {
-      if (l < cr.len) {
-        if constexpr (GATE) gi = -__expf(alog) * softplus(gi + dtb);
-        if (rs.beta_sigmoid) bi = sigmoid(bi);
-      }
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {  // inclusive prefix sum over the chunk
-        const float o = __shfl_up(gi, d);
-        if (l >= d) gi += o;
-      }
-      sm.Gs[l] = gi;
-      sm.Bs[l] = bi;
-    }
-    __syncthreads();
+template <typename T>
+__device__ __forceinline__ T lds_at(const uint8_t* base, int off) {
+  return *reinterpret_cast<const T*>(base + off);
+}
+template <typename T>
+__device__ __forceinline__ void lds_put(uint8_t* base, int off, T v) {
+  *reinterpret_cast<T*>(base + off) = v;
+}
+__device__ __forceinline__ uint2 lds_tr(const uint8_t* base, int off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) short4_t*)(base + off)));
+}
 
-    // L2 factors and per-token factors of the 64 q rows (threads 0-63) and k rows (64-127); the sum of
-    // squares runs over the stored chunks in any order
-    if (tid < 2 * CH) {
-      const int r = tid & (CH - 1);
-      const uint16_t* row = (tid < CH ? sm.u.a.Qs : sm.Ks) + r * DK;
-      float rf = 1.f;
-      if (qk_l2norm) {
-        float ss = 0.f;
+// Per-lane LDS offsets, formed once per workgroup (lane l, m = l % 16, g = l / 16).
+struct PrepLane {
+  int f16[4];    // row fragment (rows r0 + m, k = 32 kk + 8 g ..) of a 256-byte-row matrix: + 256 r0
+  int f8[2];     // the same for 128-byte rows: + 128 r0
+  int t16, t16h;  // transposing-read fragment of a 256-byte-row matrix: (t ^ 2 r0) + 8192 kk
+  int t8, t8h;   // the same for 128-byte rows: (t ^ 2 r0) + 4096 kk
+  int w32;       // transposed D-tile store, fp32 256-byte rows: (w32 ^ 64 ri) + 4096 rj
+  int w16;       // transposed D-tile store, bf16 128-byte rows: (w16 ^ 32 ri) + 2048 rj
+  int rA, rB;    // fp32 block operands of the 16x16x4 products (see mm_t)
+  int dv;        // exact-diagonal read of v rows (4 rows i0 .., 4 columns): (dv ^ 32 vb) + 4096 tb
+  __device__ __forceinline__ explicit PrepLane(int l) {
+    const int m = l & 15, g = l >> 4, s = m;
 #pragma unroll
-        for (int cc = 0; cc < DK; cc += 8) {  // chunk (cc / 8 + r) % 16: the rows' reads spread over the banks
-          const uint4 w = *reinterpret_cast<const uint4*>(row + ((cc + 8 * r) & (DK - 1)));
-          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+    for (int kk = 0; kk < 4; ++kk) f16[kk] = m * 256 + (((4 * kk + g) ^ m) << 4);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {  // both squares of a bf16 pair in one instruction (v_dot2c_f32_bf16)
-            const bf16x2 x = __builtin_bit_cast(bf16x2, u[i]);
-            ss = __builtin_amdgcn_fdot2_f32_bf16(x, x, ss, false);
-          }
-        }
-        rf = rsqrtf(ss + 1e-6f);
-      }
-      const float gr = sm.Gs[r];
-      if (tid < CH) {
-        sm.Pi[r] = scale * rf;
-        sm.Fq[r] = scale * __expf(gr) * rf;
-      } else {
-        const float br = sm.Bs[r];
-        sm.Rk[r] = rf;
-        sm.Ai[r] = br * rf;
-        sm.Fk[r] = __expf(sm.Gs[CH - 1] - gr) * rf;
-        sm.Bk[r] = br * __expf(gr) * rf;
-      }
-    }
+    for (int kk = 0; kk < 2; ++kk) f8[kk] = m * 128 + (((4 * kk + g) ^ (m >> 1)) << 4);
+    const int y16 = 8 * (g & 1) + (s >> 2);
+    t16 = (8 * g + (s >> 2)) * 256 + ((((s & 3) >> 1) ^ y16) << 4) + 8 * (s & 1);
+    t16h = (t16 + 1024) ^ 64;
+    const int y8 = 4 * (g & 1) + (s >> 3);
+    t8 = (8 * g + (s >> 2)) * 128 + ((((s & 3) >> 1) ^ y8) << 4) + 8 * (s & 1);
+    t8h = (t8 + 512) ^ 32;
+    w32 = m * 256 + ((g ^ m) << 4);
+    w16 = m * 128 + ((((g >> 1) ^ (m >> 1))) << 4) + 8 * (g & 1);
+    rA = g * 256 + ((((m >> 2) ^ g)) << 4) + (m & 3) * 4;
+    rB = m * 256 + (m << 4) + g * 4;
+    dv = (4 * g + (m >> 2)) * 256 + ((((m & 3) >> 1) ^ (4 * g + (m >> 2))) << 4) + 8 * (m & 1);
+  }
+};
 
-    // 2. K K^T and Q K^T on the 10 lower tiles each (20 tile jobs over 8 waves), kept in registers.
-    f32x4 acc[3];
+// Row fragment (rows r0 + lane%16, k-step kk) of a row-major swizzled matrix at byte `mat`.
+__device__ __forceinline__ bf16x8 pfrag16(const uint8_t* lb, int mat, int r0, int kk, const PrepLane& L) {
+  return lds_at<bf16x8>(lb, mat + 256 * r0 + L.f16[kk]);
+}
+__device__ __forceinline__ bf16x8 pfrag8(const uint8_t* lb, int mat, int r0, int kk, const PrepLane& L) {
+  return lds_at<bf16x8>(lb, mat + 128 * r0 + L.f8[kk]);
+}
+// Row fragment of M (rows r0 + lane%16 of M, k-step kk) read from M^T stored row-major (transposing reads):
+// 256-byte rows of M^T (M^T has 64 rows: k up to 64, columns up to 128) and 128-byte rows (64 columns).
+__device__ __forceinline__ bf16x8 pfragT16(const uint8_t* lb, int mat, int r0, int kk, const PrepLane& L) {
+  const uint2 a = lds_tr(lb, mat + 8192 * kk + (L.t16 ^ (2 * r0)));
+  const uint2 b = lds_tr(lb, mat + 8192 * kk + (L.t16h ^ (2 * r0)));
+  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+__device__ __forceinline__ bf16x8 pfragT8(const uint8_t* lb, int mat, int r0, int kk, const PrepLane& L) {
+  const uint2 a = lds_tr(lb, mat + 4096 * kk + (L.t8 ^ (2 * r0)));
+  const uint2 b = lds_tr(lb, mat + 4096 * kk + (L.t8h ^ (2 * r0)));
+  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+// D tile (rows 16 ri + 4 (lane/16) + i, column 16 rj + lane%16) stored transposed: fp32 into 256-byte rows,
+// bf16 (4 values, 8 bytes) into 128-byte rows.
+__device__ __forceinline__ void put_t32(uint8_t* lb, int mat, int ri, int rj, const PrepLane& L, f32x4 d) {
+  lds_put<f32x4>(lb, mat + 4096 * rj + (L.w32 ^ (64 * ri)), d);
+}
+__device__ __forceinline__ void put_t16(uint8_t* lb, int mat, int ri, int rj, const PrepLane& L, f32x4 d) {
+  lds_put<uint2>(lb, mat + 2048 * rj + (L.w16 ^ (32 * ri)), make_uint2(pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])));
+}
+// acc += X[bi][bj] . Y[ci][cj] for 16x16 fp32 blocks of matrices stored transposed (X^T, Y^T row-major,
+// 256-byte rows, fp32 swizzle), on v_mfma_f32_16x16x4_f32: A element X[16 bi + m][16 bj + 4 s + g] at row
+// 16 bj + 4 s + g, column 16 bi + m of X^T; B element Y[16 ci + 4 s + g][16 cj + m] at row 16 cj + m, column
+// 16 ci + 4 s + g of Y^T. `sub` (nonnegative mat2): A element X - X2[b2i][b2j].
+__device__ __forceinline__ float lA(const uint8_t* lb, int mat, int bi, int bj, int s, const PrepLane& L) {
+  return lds_at<float>(lb, mat + 4096 * bj + 1024 * s + ((bi ^ s) << 6) + L.rA);
+}
+__device__ __forceinline__ float lB(const uint8_t* lb, int mat, int ci, int cj, int s, const PrepLane& L) {
+  return lds_at<float>(lb, mat + 4096 * cj + (L.rB ^ ((4 * ci ^ s) << 4)));
+}
+__device__ __forceinline__ f32x4 mm_t(const uint8_t* lb, int xm, int bi, int bj, int ym, int ci, int cj,
+                                      const PrepLane& L, f32x4 acc) {
 #pragma unroll
-    for (int m = 0; m < 3; ++m) {
-      const int job = wave + P1_WAVES * m;
-      acc[m] = zero4();
-      if (job < 20) {
-        int rb, cb;
-        lower_tile(job % 10, rb, cb);
-        acc[m] = stile<16, 16>(job < 10 ? sm.Ks : sm.u.a.Qs, rb * 16, sm.Ks, cb * 16, DK, sw, zero4());
-      }
-    }
-    __syncthreads();  // As / Ts overwrite Qs / Ks; the per-token factors are visible
-    // A_ij = beta_i rk_i exp(G_i - G_j) rk_j k_i.k_j (i > j), P_ij = s rq_i exp(G_i - G_j) rk_j q_i.k_j (i >= j)
+  for (int s = 0; s < 4; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(lA(lb, xm, bi, bj, s, L), lB(lb, ym, ci, cj, s, L), acc, 0, 0, 0);
+  return acc;
+}
+__device__ __forceinline__ f32x4 mm_t_diff(const uint8_t* lb, int xm, int bi, int bj, int x2m, int b2i, int b2j,
+                                           int ym, int ci, int cj, const PrepLane& L, f32x4 acc) {
 #pragma unroll
-    for (int m = 0; m < 3; ++m) {
-      const int job = wave + P1_WAVES * m;
-      if (job < 20) {
-        int rb, cb;
-        lower_tile(job % 10, rb, cb);
-        const int j = cb * 16 + (l & 15), i0 = rb * 16 + 4 * (l >> 4);
-        const float gj = sm.Gs[j], rkj = sm.Rk[j];
-        const float4 gi = *reinterpret_cast<const float4*>(&sm.Gs[i0]);
-        const float4 fi = *reinterpret_cast<const float4*>(job < 10 ? &sm.Ai[i0] : &sm.Pi[i0]);
-        const float gv[4] = {gi.x, gi.y, gi.z, gi.w}, fv[4] = {fi.x, fi.y, fi.z, fi.w};
-        float e[4];
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) e[i4] = fv[i4] * __expf(gv[i4] - gj) * rkj * acc[m][i4];
-        if (job < 10) {
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) sm.u.b.As[at32<16>(i0 + i4, j)] = i0 + i4 > j ? e[i4] : 0.f;
-        } else {
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) sm.Ps[at16<8>(i0 + i4, j)] = f32_to_bf16(i0 + i4 >= j ? e[i4] : 0.f);
-        }
-      }
-    }
-    zero_upper_blocks(sm.Ps);
-    __syncthreads();
+  for (int s = 0; s < 4; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(lA(lb, xm, bi, bj, s, L) - lA(lb, x2m, b2i, b2j, s, L),
+                                                lB(lb, ym, ci, cj, s, L), acc, 0, 0, 0);
+  return acc;
+}
 
-    // 3a. diagonal 16x16 blocks of T by forward substitution (one wave; lane = 16 * block + column).
-    if (wave == 0) {
-      const int b = l >> 4, col = l & 15, base = b * 16;
-      float t[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float a[16];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 x = *reinterpret_cast<const float4*>(&sm.u.b.As[at32<16>(base + r, base + 4 * q4)]);
-          a[4 * q4] = x.x; a[4 * q4 + 1] = x.y; a[4 * q4 + 2] = x.z; a[4 * q4 + 3] = x.w;
-        }
-        // two interleaved partial sums keep the dependent chain short
-        float s0 = (r == col) ? 1.f : 0.f, s1 = 0.f;
-#pragma unroll
-        for (int jj = 0; jj + 1 < r; jj += 2) {
-          s0 = fmaf(-a[jj], t[jj], s0);
-          s1 = fmaf(-a[jj + 1], t[jj + 1], s1);
-        }
-        if (r & 1) s0 = fmaf(-a[r - 1], t[r - 1], s0);
-        t[r] = s0 + s1;
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sm.u.b.Ts[at32<16>(base + r, base + col)] = t[r];
-    }
-    __syncthreads();
+// Buffer resource over rows [t0, t0 + len) of a row-major bf16 array (row stride `ld` elements), starting at
+// column `col`: a row's byte at (row - t0) * 2 ld + 2 (c - col); rows from len on read zero.
+__device__ __forceinline__ Rsrc rows_rsrc(const uint16_t* p, long t0, long ld, int col, int len) {
+  return raw_rsrc(p + t0 * ld + col, (uint32_t)(len > 0 ? len : 0) * (uint32_t)ld * 2u);
+}
 
-    // 3b. off-diagonal blocks. With N_ij = T_ii A_ij (i > j) the block recurrence T_ij = -sum_m N_im T_mj
-    // unrolls to T_10 = -N_10 T_00, T_21 = -N_21 T_11, T_32 = -N_32 T_22, T_20 = (N_21 N_10 - N_20) T_00,
-    // T_31 = (N_32 N_21 - N_31) T_11 and T_30 = (N_32 N_20 - N_30) T_00 + (N_32 N_21 - N_31) T_10: three levels
-    // of 16x16 fp32 MFMA block products (a chain of four instead of nine). N overwrites A's blocks; the pair
-    // products sit in T's (unused) blocks above the diagonal.
-    if (wave < 6) {  // level 1: N_ij, one block a wave
-      const int bi = wave < 1 ? 1 : (wave < 3 ? 2 : 3), bj = wave - bi * (bi - 1) / 2;
-      put16_f32(sm.u.b.As, 16 * bi, 16 * bj, l,
-                mm16_f32(sm.u.b.Ts, 16 * bi, 16 * bi, sm.u.b.As, 16 * bi, 16 * bj, l, zero4()), false);
-    }
-    __syncthreads();
-    if (wave < 3) {  // level 2: T_10, T_21, T_32
-      put16_f32(sm.u.b.Ts, 16 * (wave + 1), 16 * wave, l,
-                mm16_f32(sm.u.b.As, 16 * (wave + 1), 16 * wave, sm.u.b.Ts, 16 * wave, 16 * wave, l, zero4()), true);
-    } else if (wave < 6) {  // N_21 N_10 -> T(0,1), N_32 N_20 -> T(0,2), N_32 N_21 -> T(0,3)
-      const int ai = wave == 3 ? 2 : 3, aj = wave == 3 ? 1 : 2, bi = wave == 3 ? 1 : 2, bj = wave == 5 ? 1 : 0;
-      put16_f32(sm.u.b.Ts, 0, 16 * (wave - 2), l,
-                mm16_f32(sm.u.b.As, 16 * ai, 16 * aj, sm.u.b.As, 16 * bi, 16 * bj, l, zero4()), false);
-    }
-    __syncthreads();
-    if (wave < 3) {  // level 3: T_20, T_31, T_30
-      if (wave == 0) {
-        put16_f32(sm.u.b.Ts, 32, 0, l, mm16_f32_diff(sm.u.b.Ts, 0, 16, sm.u.b.As, 32, 0, sm.u.b.Ts, 0, 0, l, zero4()), false);
-      } else if (wave == 1) {
-        put16_f32(sm.u.b.Ts, 48, 16, l, mm16_f32_diff(sm.u.b.Ts, 0, 48, sm.u.b.As, 48, 16, sm.u.b.Ts, 16, 16, l, zero4()), false);
-      } else {
-        f32x4 t = mm16_f32_diff(sm.u.b.Ts, 0, 32, sm.u.b.As, 48, 0, sm.u.b.Ts, 0, 0, l, zero4());
-        t = mm16_f32_diff(sm.u.b.Ts, 0, 48, sm.u.b.As, 48, 16, sm.u.b.Ts, 16, 0, l, t);
-        put16_f32(sm.u.b.Ts, 48, 0, l, t, false);
-      }
-    }
-    __syncthreads();
+struct RowRegs {
+  uint4 q0, q1, k0, k1, v0, v1;
+};
 
-    // 3c. the bf16 forms of T, in 2x2 blocks (through registers: they overwrite A and T): TBF = diag(Fk) T
-    // diag(Bk), TBT = (T diag(Bk))^T, LB = (T - I) diag(beta). (T above the diagonal blocks is masked.)
-    {
-      uint32_t wf[2][2], wt[2][2], wl[2][2];
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int e = tid + P1_THREADS * m;
-        const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
-        const float2 ta = *reinterpret_cast<const float2*>(&sm.u.b.Ts[at32<16>(i, j)]);
-        const float2 tc = *reinterpret_cast<const float2*>(&sm.u.b.Ts[at32<16>(i + 1, j)]);
-        const float t00 = i >= j ? ta.x : 0.f, t01 = i > j ? ta.y : 0.f;
-        const float t10 = i + 1 >= j ? tc.x : 0.f, t11 = i >= j ? tc.y : 0.f;
-        const float2 bk = *reinterpret_cast<const float2*>(&sm.Bk[j]);
-        const float2 bs = *reinterpret_cast<const float2*>(&sm.Bs[j]);
-        const float2 fk = *reinterpret_cast<const float2*>(&sm.Fk[i]);
-        const float b00 = t00 * bk.x, b01 = t01 * bk.y, b10 = t10 * bk.x, b11 = t11 * bk.y;
-        wf[m][0] = pack_bf16x2(fk.x * b00, fk.x * b01);
-        wf[m][1] = pack_bf16x2(fk.y * b10, fk.y * b11);
-        wt[m][0] = pack_bf16x2(b00, b10);
-        wt[m][1] = pack_bf16x2(b01, b11);
-        wl[m][0] = pack_bf16x2(i > j ? t00 * bs.x : 0.f, i > j + 1 ? t01 * bs.y : 0.f);
-        wl[m][1] = pack_bf16x2(i + 1 > j ? t10 * bs.x : 0.f, i > j ? t11 * bs.y : 0.f);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int e = tid + P1_THREADS * m;
-        const int i = 2 * (e / (CH / 2)), j = 2 * (e % (CH / 2));
-        *reinterpret_cast<uint32_t*>(&sm.u.c.TBF[at16<8>(i, j)]) = wf[m][0];
-        *reinterpret_cast<uint32_t*>(&sm.u.c.TBF[at16<8>(i + 1, j)]) = wf[m][1];
-        *reinterpret_cast<uint32_t*>(&sm.u.c.TBT[at16<8>(j, i)]) = wt[m][0];
-        *reinterpret_cast<uint32_t*>(&sm.u.c.TBT[at16<8>(j + 1, i)]) = wt[m][1];
-        *reinterpret_cast<uint32_t*>(&sm.u.c.LB[at16<8>(i, j)]) = wl[m][0];
-        *reinterpret_cast<uint32_t*>(&sm.u.c.LB[at16<8>(i + 1, j)]) = wl[m][1];
-      }
-    }
-    __syncthreads();
+// The chunk's rows of q, k, v for thread (rr, c8): rows rr and rr + 32, columns c8 .. c8 + 7 (zeros past the
+// chunk end).
+__device__ __forceinline__ void load_rows(RowRegs& R, int item, const uint16_t* q, const uint16_t* k,
+                                          const uint16_t* v, const int32_t* cu, const int32_t* chunk_idx, int n_seqs,
+                                          int T, int Hk, int Hv, const RowStrides& rs, uint32_t oq, uint32_t ok,
+                                          uint32_t ov) {
+  const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
+  const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+  const Rsrc rq = rows_rsrc(q, cr.t0, rs.q, hk * DK, cr.len), rk = rows_rsrc(k, cr.t0, rs.k, hk * DK, cr.len);
+  const Rsrc rv = rows_rsrc(v, cr.t0, rs.v, h * DV, cr.len);
+  R.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq, 0, 0));
+  R.k0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok, 0, 0));
+  R.v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, ov, 0, 0));
+  R.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq + 64u * (uint32_t)rs.q, 0, 0));
+  R.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 64u * (uint32_t)rs.k, 0, 0));
+  R.v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, ov + 64u * (uint32_t)rs.v, 0, 0));
+}
 
-    // raw q of this wave's Q' jobs (step 5), loaded now so the latency is covered by step 4
-    uint2 cq[2][2];
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3;
-      const int tok = 16 * tb + (l & 15);
-      cq[m][0] = cq[m][1] = make_uint2(0, 0);
-      if (tok < cr.len) {
-        const uint16_t* qrow = q + (size_t)(cr.t0 + tok) * rs.q + hk * DK + 32 * kq + 4 * (l >> 4);
-        cq[m][0] = *reinterpret_cast<const uint2*>(qrow);
-        cq[m][1] = *reinterpret_cast<const uint2*>(qrow + 16);
-      }
-    }
-
-    // 4a. W' (as A fragments), R = P T diag(Bk), and the K^T fragments.
-    {
-      uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {  // (token tile, k-step): W'^T = K^T TBF^T
-        const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        const f32x4 d0 = stile_ta(sm.Ks, 32 * kq, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
-        const f32x4 d1 = stile_ta(sm.Ks, 32 * kq + 16, sm.u.c.TBF, 16 * tb, kend, sw, zero4());
-        gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
-      }
-      for (int job = wave; job < 10; job += P1_WAVES) {  // R = P TB on the lower tiles
-        int rb, cb;
-        lower_tile(job, rb, cb);
-        const f32x4 r = stile<8, 8>(sm.Ps, 16 * rb, sm.u.c.TBT, 16 * cb, tri_kend(rb), sw, zero4());
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) sm.u.c.Rs[at16<8>(16 * rb + 4 * (l >> 4) + i4, 16 * cb + (l & 15))] = f32_to_bf16(r[i4]);
-      }
-      zero_upper_blocks(sm.u.c.Rs);
-      uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
-#pragma unroll
-      for (int m = 0; m < DK * CH / 8 / P1_THREADS; ++m) {  // fragment f = 2 w + kk, lane ll
-        const int e = tid + P1_THREADS * m;
-        const int f = e >> 6, ll = e & 63, w = f >> 1, kk = f & 1;
-        gKT[e] = __builtin_bit_cast(uint4, tfrag(sm.Ks, 16 * w, kk));
-        (void)ll;
-      }
-    }
-    __syncthreads();  // Ub^T overwrites TBF, TBT
-
-    // 4b. Ub = beta V + LB V: Ub' = Fk Ub (D tiles, fp32) to the workspace, Ub^T (bf16) to LDS.
-    {
-      float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {  // (token tile, value block)
-        const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
-        const f32x4 u = stile_tb(sm.u.c.LB, 16 * tb, sm.Vs, 16 * vb, tri_kend(tb), sw, zero4());
-        const int n = vb * 16 + (l & 15), i0 = tb * 16 + 4 * (l >> 4);
-        // v[i0 .. i0+3][n] by one transposing read (lane s: row i0 + s/4, columns 16 vb + 4 (s%4) ..)
-        const uint2 vv = __builtin_bit_cast(
-            uint2, lds_read_tr(sm.Vs + at16<16>(i0 + ((l & 15) >> 2), vb * 16 + 4 * (l & 3))));
-        const float4 bs = *reinterpret_cast<const float4*>(&sm.Bs[i0]);
-        const float4 fk = *reinterpret_cast<const float4*>(&sm.Fk[i0]);
-        float ub[4];
-        ub[0] = fmaf(bs.x, __uint_as_float(vv.x << 16), u[0]);
-        ub[1] = fmaf(bs.y, __uint_as_float(vv.x & 0xffff0000u), u[1]);
-        ub[2] = fmaf(bs.z, __uint_as_float(vv.y << 16), u[2]);
-        ub[3] = fmaf(bs.w, __uint_as_float(vv.y & 0xffff0000u), u[3]);
-        gU[(vb * 4 + tb) * 64 + l] = make_float4(fk.x * ub[0], fk.y * ub[1], fk.z * ub[2], fk.w * ub[3]);
-        *reinterpret_cast<uint2*>(&sm.u.UbT[at16<8>(n, i0)]) = make_uint2(pack_bf16x2(ub[0], ub[1]), pack_bf16x2(ub[2], ub[3]));
-      }
-    }
-    __syncthreads();
-
-    // 5. Q' = Fq q - R K (as A fragments) and Ob = P Ub (D tiles, bf16); G_L.
-    {
-      uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {  // (token tile, k-step): Q'^T = Fq q^T - K^T R^T
-        const int job = wave + P1_WAVES * m, tb = job >> 2, kq = job & 3, kend = tri_kend(tb);
-        f32x4 d0 = stile_ta(sm.Ks, 32 * kq, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
-        f32x4 d1 = stile_ta(sm.Ks, 32 * kq + 16, sm.u.c.Rs, 16 * tb, kend, sw, zero4());
-        const float fq = sm.Fq[16 * tb + (l & 15)];
-        const uint2 c0 = cq[m][0], c1 = cq[m][1];
-        d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
-        d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
-        d0[2] = fmaf(fq, __uint_as_float(c0.y << 16), -d0[2]);
-        d0[3] = fmaf(fq, __uint_as_float(c0.y & 0xffff0000u), -d0[3]);
-        d1[0] = fmaf(fq, __uint_as_float(c1.x << 16), -d1[0]);
-        d1[1] = fmaf(fq, __uint_as_float(c1.x & 0xffff0000u), -d1[1]);
-        d1[2] = fmaf(fq, __uint_as_float(c1.y << 16), -d1[2]);
-        d1[3] = fmaf(fq, __uint_as_float(c1.y & 0xffff0000u), -d1[3]);
-        gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
-      }
-      uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {  // (token tile, value block): Ob = P Ub
-        const int job = wave + P1_WAVES * m, tb = job >> 3, vb = job & 7;
-        const f32x4 y = stile<8, 8>(sm.Ps, 16 * tb, sm.u.UbT, 16 * vb, tri_kend(tb), sw, zero4());
-        gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
-      }
-      if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = sm.Gs[CH - 1];
-    }
-    __syncthreads();  // the next item's rows overwrite Qs (aliasing Rs / Ub^T), Ks and Vs
+// Once per workgroup: the blocks of P^T that stay zero (P's blocks above its diagonal blocks).
+__device__ __forceinline__ void prep_init(uint8_t* lb) {
+  // P^T physical blocks (pr, pc) with pr > pc: (1,0), (2,0), (2,1), (3,0), (3,1), (3,2); 512 bytes each
+  for (int e = threadIdx.x; e < 6 * 32; e += P1_THREADS) {
+    const int t = e >> 5, w = e & 31;
+    const int pr = t < 1 ? 1 : (t < 3 ? 2 : 3), pc = t - pr * (pr - 1) / 2;
+    const int row = 16 * pr + (w >> 1), c8 = 16 * pc + 8 * (w & 1);  // 8 bf16 of a row
+    lds_put<uint4>(lb, PS_PT + row * 128 + ((((c8 >> 3) ^ ((row >> 1) & 7))) << 4), make_uint4(0, 0, 0, 0));
   }
 }
 
-// Persistent over items (chunk x head, chunk-major): each workgroup processes items blockIdx.x, + gridDim.x, ...
-// Two workgroups share a CU, so one's loads and barriers overlap the other's work.
+// Workgroup barrier over the item's LDS traffic only: it waits for this wave's LDS accesses, not for its
+// global loads and stores (the next item's rows, the workspace stores stay in flight across it; nothing of the
+// workspace is read back by the item).
+__device__ __forceinline__ void item_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One phase-1 item. `R` holds the item's rows (loaded by the caller); `next` (>= 0) is the item whose rows
+// are loaded into R while this one computes. Ends with a workgroup barrier.
+template <typename TG, bool GATE>
+__device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int next,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
+    int n_seqs, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides& rs,
+    uint8_t* __restrict__ ws, const PrepLane& L0, int rowoff, uint32_t oq, uint32_t ok, uint32_t ov) {
+  // the lane offsets pass through an empty asm per item: the compiler then forms the addresses derived from
+  // them inside the item (most fold into instruction offsets) instead of hoisting every one of them out of the
+  // item loop, where they would not fit the registers
+  PrepLane L = L0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(L.f16[i]));
+  asm volatile("" : "+v"(L.f8[0]), "+v"(L.f8[1]), "+v"(L.t16), "+v"(L.t16h), "+v"(L.t8), "+v"(L.t8h));
+  asm volatile("" : "+v"(L.w32), "+v"(L.w16), "+v"(L.rA), "+v"(L.rB), "+v"(L.dv), "+v"(rowoff));
+  int tid = threadIdx.x;  // (opaque per item as well, for the values derived from it)
+  asm volatile("" : "+v"(tid));
+  const int l = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m = l & 15, gq = l >> 4;
+  const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
+  const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+  uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
+  float* F = reinterpret_cast<float*>(lb + PS_F);
+
+  // gate inputs (wave 7), issued before the row stores
+  float gi = 0.f, bi = 0.f, alog = 0.f, dtb = 0.f;
+  if (wave == P1_WAVES - 1 && l < cr.len) {
+    const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
+    gi = io<TG>::load(g + gh);
+    bi = io<TG>::load(beta + gh);
+    if constexpr (GATE) {
+      alog = A_log[h];
+      dtb = dt_bias[h];
+    }
+  }
+  // 1. rows -> LDS; the next item's rows into the registers
+  lds_put<uint4>(lb, PS_Q + rowoff, R.q0);
+  lds_put<uint4>(lb, PS_Q + rowoff + 8192, R.q1);
+  lds_put<uint4>(lb, PS_K + rowoff, R.k0);
+  lds_put<uint4>(lb, PS_K + rowoff + 8192, R.k1);
+  lds_put<uint4>(lb, PS_V + rowoff, R.v0);
+  lds_put<uint4>(lb, PS_V + rowoff + 8192, R.v1);
+  if (next >= 0) load_rows(R, next, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, oq, ok, ov);
+  if (wave == P1_WAVES - 1) {
+    if (l < cr.len) {
+      if constexpr (GATE) gi = -__expf(alog) * softplus(gi + dtb);
+      if (rs.beta_sigmoid) bi = sigmoid(bi);
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float o = __shfl_up(gi, d);
+      if (l >= d) gi += o;
+    }
+    F[(PSF_G >> 2) + l] = gi;
+    F[(PSF_B >> 2) + l] = bi;
+  }
+  item_barrier();
+
+  // 2. factors (threads 0-127: q rows, then k rows) and the K K^T / Q K^T tiles. Wave 0 takes the 4 diagonal
+  // K K^T tiles (it inverts those blocks next); waves 1-7 take the other 16 tiles (jobs j: 0-5 the K K^T tiles
+  // below the diagonal blocks, 6-15 the Q K^T tiles on and below them).
+  if (tid < 2 * CH) {
+    const int r = tid & (CH - 1);
+    const int mat = tid < CH ? PS_Q : PS_K;
+    float rf = 1.f;
+    if (qk_l2norm) {
+      float ss = 0.f;
+      const int base = mat + r * 256 + ((r & 15) << 4);
+#pragma unroll
+      for (int cc = 0; cc < 16; ++cc) {  // physical chunk cc ^ (r % 16): every lane of 16 on its own banks
+        const uint4 w4 = lds_at<uint4>(lb, base ^ (cc << 4));
+        const uint32_t u[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bf16x2 x = __builtin_bit_cast(bf16x2, u[i]);
+          ss = __builtin_amdgcn_fdot2_f32_bf16(x, x, ss, false);
+        }
+      }
+      rf = rsqrtf(ss + 1e-6f);
+    }
+    const float gr = F[(PSF_G >> 2) + r];
+    if (tid < CH) {
+      F[(PSF_PI >> 2) + r] = scale * rf;
+      F[(PSF_FQ >> 2) + r] = scale * __expf(gr) * rf;
+    } else {
+      const float br = F[(PSF_B >> 2) + r];
+      F[(PSF_RK >> 2) + r] = rf;
+      F[(PSF_AI >> 2) + r] = br * rf;
+      F[(PSF_FK >> 2) + r] = __expf(F[(PSF_G >> 2) + CH - 1] - gr) * rf;
+      F[(PSF_BK >> 2) + r] = br * __expf(gr) * rf;
+    }
+  }
+  f32x4 acc[4];
+  int jrb[3], jcb[3];
+  bool jqk[3];
+  if (wave == 0) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      acc[b] = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 f = pfrag16(lb, PS_K, 16 * b, kk, L);
+        acc[b] = mfma(f, f, acc[b]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      const int j = wave - 1 + 7 * n;
+      jrb[n] = jcb[n] = 0;
+      jqk[n] = false;
+      acc[n] = zero4();
+      if (j < 16) {
+        int rb, cb;
+        if (j < 6) {
+          rb = j < 1 ? 1 : (j < 3 ? 2 : 3);
+          cb = j - rb * (rb - 1) / 2;
+        } else {
+          lower_tile(j - 6, rb, cb);
+        }
+        jrb[n] = rb;
+        jcb[n] = cb;
+        jqk[n] = j >= 6;
+        const int am = j >= 6 ? PS_Q : PS_K;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          acc[n] = mfma(pfrag16(lb, am, 16 * rb, kk, L), pfrag16(lb, PS_K, 16 * cb, kk, L), acc[n]);
+      }
+    }
+  }
+  item_barrier();  // A^T overwrites the q rows; the factors are visible
+
+  // 3. scaled tiles -> A^T (fp32) and P^T (bf16); wave 0: the diagonal blocks, then their inverse
+  // A_ij = beta_i rk_i exp(G_i - G_j) rk_j k_i.k_j (i > j), P_ij = s rq_i exp(G_i - G_j) rk_j q_i.k_j (i >= j)
+  auto scale_tile = [&](f32x4 a, int rb, int cb, bool qk) {
+    const int j = 16 * cb + m, i0 = 16 * rb + 4 * gq;
+    const float gj = F[(PSF_G >> 2) + j], rkj = F[(PSF_RK >> 2) + j];
+    const f32x4 gi4 = lds_at<f32x4>(lb, PS_F + PSF_G + 4 * i0);
+    const f32x4 fi4 = lds_at<f32x4>(lb, PS_F + (qk ? PSF_PI : PSF_AI) + 4 * i0);
+    f32x4 e;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = fi4[r] * __expf(gi4[r] - gj) * rkj * a[r];
+      e[r] = (qk ? i0 + r >= j : i0 + r > j) ? x : 0.f;
+    }
+    return e;
+  };
+  if (wave == 0) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) put_t32(lb, PS_AT, b, b, L, scale_tile(acc[b], b, b, false));
+    wave_sync_lds();
+    // right-looking substitution: lane (block gq, column m); s[r] -> T_b[r][m]
+    float sv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] = r == m ? 1.f : 0.f;
+    const int rowb = PS_AT + gq * 4096 + ((4 * gq) << 4);  // row 16 gq of A^T, chunk 4 gq (before the XORs)
+    // the row of A^T for step mm (column mm of the block) is read one step ahead, only its chunks that hold
+    // rows below mm
+    f32x4 a4[4], n4[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) a4[qd] = lds_at<f32x4>(lb, (rowb ^ (qd << 4)));
+#pragma unroll
+    for (int mm = 0; mm < 15; ++mm) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+        if (mm + 1 < 15 && 4 * qd + 3 > mm + 1) n4[qd] = lds_at<f32x4>(lb, (rowb ^ ((qd ^ (mm + 1)) << 4)) + (mm + 1) * 256);
+      const float t = sv[mm];
+#pragma unroll
+      for (int r = mm + 1; r < 16; ++r) sv[r] = fmaf(-a4[r >> 2][r & 3], t, sv[r]);
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+        if (4 * qd + 3 > mm + 1) a4[qd] = n4[qd];
+    }
+    // column m of T_b -> row 16 gq + m of T^T, columns 16 gq .. + 15
+    const int roww = PS_TT + (16 * gq + m) * 256 + (((4 * gq) ^ m) << 4);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+      lds_put<f32x4>(lb, roww ^ (qd << 4), f32x4{sv[4 * qd], sv[4 * qd + 1], sv[4 * qd + 2], sv[4 * qd + 3]});
+  } else {
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (wave - 1 + 7 * n < 16) {
+        const f32x4 e = scale_tile(acc[n], jrb[n], jcb[n], jqk[n]);
+        if (jqk[n]) put_t16(lb, PS_PT, jrb[n], jcb[n], L, e);
+        else put_t32(lb, PS_AT, jrb[n], jcb[n], L, e);
+      }
+    }
+  }
+  item_barrier();
+
+  // 4. off-diagonal blocks of T: N_ij = T_ii A_ij (i > j, into A's blocks), then T_10, T_21, T_32 and the
+  // pair products N_21 N_10, N_32 N_20, N_32 N_21 (into T's blocks (0, 1..3)), then T_20, T_31, T_30
+  if (wave < 6) {
+    const int i = wave < 1 ? 1 : (wave < 3 ? 2 : 3), j = wave - i * (i - 1) / 2;
+    put_t32(lb, PS_AT, i, j, L, mm_t(lb, PS_TT, i, i, PS_AT, i, j, L, zero4()));
+  }
+  item_barrier();
+  if (wave < 3) {
+    put_t32(lb, PS_TT, wave + 1, wave, L, -mm_t(lb, PS_AT, wave + 1, wave, PS_TT, wave, wave, L, zero4()));
+  } else if (wave < 6) {
+    const int ai = wave == 3 ? 2 : 3, aj = wave == 3 ? 1 : 2, ci = wave == 3 ? 1 : 2, cj = wave == 5 ? 1 : 0;
+    put_t32(lb, PS_TT, 0, wave - 2, L, mm_t(lb, PS_AT, ai, aj, PS_AT, ci, cj, L, zero4()));
+  }
+  item_barrier();
+  if (wave == 0) {
+    put_t32(lb, PS_TT, 2, 0, L, mm_t_diff(lb, PS_TT, 0, 1, PS_AT, 2, 0, PS_TT, 0, 0, L, zero4()));
+  } else if (wave == 1) {
+    put_t32(lb, PS_TT, 3, 1, L, mm_t_diff(lb, PS_TT, 0, 3, PS_AT, 3, 1, PS_TT, 1, 1, L, zero4()));
+  } else if (wave == 2) {
+    f32x4 t = mm_t_diff(lb, PS_TT, 0, 2, PS_AT, 3, 0, PS_TT, 0, 0, L, zero4());
+    t = mm_t_diff(lb, PS_TT, 0, 3, PS_AT, 3, 1, PS_TT, 1, 0, L, t);
+    put_t32(lb, PS_TT, 3, 0, L, t);
+  }
+  item_barrier();
+
+  // 5. bf16 forms, row by row of T^T (row j = column j of T; 8 columns i0 .. i0 + 7 a thread):
+  // TBF^T[j][i] = Fk_i T_ij... = Fk_i T[i][j] Bk_j, TBT[j][i] = T[i][j] Bk_j, LB^T[j][i] = (T - I)[i][j] beta_j;
+  // T's blocks above its diagonal blocks (pair products there) are zero
+  {
+    const int j = tid >> 3, i0 = (tid & 7) * 8;
+    const int rd = PS_TT + j * 256 + (((2 * (tid & 7)) ^ (j & 15)) << 4);
+    f32x4 t0 = lds_at<f32x4>(lb, rd), t1 = lds_at<f32x4>(lb, rd ^ 16);
+    if ((i0 >> 4) < (j >> 4)) t0 = t1 = zero4();
+    const float bkj = F[(PSF_BK >> 2) + j], bj = F[(PSF_B >> 2) + j];
+    const f32x4 fk0 = lds_at<f32x4>(lb, PS_F + PSF_FK + 4 * i0), fk1 = lds_at<f32x4>(lb, PS_F + PSF_FK + 4 * i0 + 16);
+    const float tv[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+    const float fk[8] = {fk0[0], fk0[1], fk0[2], fk0[3], fk1[0], fk1[1], fk1[2], fk1[3]};
+    uint32_t wf[4], wt[4], wl[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float b0 = tv[2 * p] * bkj, b1 = tv[2 * p + 1] * bkj;
+      wf[p] = pack_bf16x2(fk[2 * p] * b0, fk[2 * p + 1] * b1);
+      wt[p] = pack_bf16x2(b0, b1);
+      wl[p] = pack_bf16x2(i0 + 2 * p == j ? 0.f : tv[2 * p] * bj, i0 + 2 * p + 1 == j ? 0.f : tv[2 * p + 1] * bj);
+    }
+    item_barrier();  // the forms overwrite T^T and A^T
+    const int wr = j * 128 + ((((tid & 7) ^ ((j >> 1) & 7))) << 4);
+    lds_put<uint4>(lb, PS_TBF + wr, make_uint4(wf[0], wf[1], wf[2], wf[3]));
+    lds_put<uint4>(lb, PS_TBT + wr, make_uint4(wt[0], wt[1], wt[2], wt[3]));
+    lds_put<uint4>(lb, PS_LB + wr, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+  }
+  item_barrier();
+
+  // raw q of this wave's Q' jobs (step 8), loaded now so the latency is covered
+  uint2 cq[2][2];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
+    const int tok = 16 * tb + m;
+    cq[n][0] = cq[n][1] = make_uint2(0, 0);
+    if (tok < cr.len) {
+      const uint16_t* qrow = q + (size_t)(cr.t0 + tok) * rs.q + hk * DK + 32 * kq + 4 * gq;
+      cq[n][0] = *reinterpret_cast<const uint2*>(qrow);
+      cq[n][1] = *reinterpret_cast<const uint2*>(qrow + 16);
+    }
+  }
+
+  // 6. W'^T = K^T TBF^T (A fragments to the workspace), R = P TB (as R^T; R's blocks above its diagonal
+  // blocks zero), the K^T fragments
+  {
+    uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
+      f32x4 d0 = zero4(), d1 = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        if (kk < nk) {
+          const bf16x8 bf = pfragT8(lb, PS_TBF, 16 * tb, kk, L);
+          d0 = mfma(pfragT16(lb, PS_K, 32 * kq, kk, L), bf, d0);
+          d1 = mfma(pfragT16(lb, PS_K, 32 * kq + 16, kk, L), bf, d1);
+        }
+      gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {  // R tiles: jobs 0-9 the lower tiles, 10-15 zero tiles above
+      const int job = wave + P1_WAVES * n;
+      int rb, cb;
+      if (job < 10) {
+        lower_tile(job, rb, cb);
+        f32x4 r = zero4();
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          if (kk < tri_kend(rb) / 32) r = mfma(pfragT8(lb, PS_PT, 16 * rb, kk, L), pfrag8(lb, PS_TBT, 16 * cb, kk, L), r);
+        put_t16(lb, PS_RT, rb, cb, L, r);
+      } else {
+        const int t = job - 10;  // (rb, cb) with rb < cb: (0,1) (0,2) (1,2) (0,3) (1,3) (2,3)
+        cb = t < 1 ? 1 : (t < 3 ? 2 : 3);
+        rb = t - cb * (cb - 1) / 2;
+        put_t16(lb, PS_RT, rb, cb, L, zero4());
+      }
+    }
+    uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {  // fragment f = 2 w + kk = wave + 8 n (16 fragments of 64 lanes)
+      const int f = wave + P1_WAVES * n;
+      gKT[f * 64 + l] = __builtin_bit_cast(uint4, pfragT16(lb, PS_K, 16 * (f >> 1), f & 1, L));
+    }
+  }
+  item_barrier();  // Ub^T overwrites TBF, TBT
+
+  // 7. Ub = beta V + LB V: Ub' = Fk Ub (fp32 D tiles) to the workspace, Ub^T (bf16) to LDS
+  {
+    float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
+    const int vb = wave;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 u = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        if (kk < tri_kend(tb) / 32) u = mfma(pfragT8(lb, PS_LB, 16 * tb, kk, L), pfragT16(lb, PS_V, 16 * vb, kk, L), u);
+      const int i0 = 16 * tb + 4 * gq;
+      const uint2 vv = lds_tr(lb, PS_V + 4096 * tb + (L.dv ^ (32 * vb)));
+      const f32x4 bs = lds_at<f32x4>(lb, PS_F + PSF_B + 4 * i0);
+      const f32x4 fk = lds_at<f32x4>(lb, PS_F + PSF_FK + 4 * i0);
+      f32x4 ub;
+      ub[0] = fmaf(bs[0], __uint_as_float(vv.x << 16), u[0]);
+      ub[1] = fmaf(bs[1], __uint_as_float(vv.x & 0xffff0000u), u[1]);
+      ub[2] = fmaf(bs[2], __uint_as_float(vv.y << 16), u[2]);
+      ub[3] = fmaf(bs[3], __uint_as_float(vv.y & 0xffff0000u), u[3]);
+      gU[(vb * 4 + tb) * 64 + l] = make_float4(fk[0] * ub[0], fk[1] * ub[1], fk[2] * ub[2], fk[3] * ub[3]);
+      put_t16(lb, PS_UBT, tb, vb, L, ub);
+    }
+  }
+  item_barrier();
+
+  // 8. Q' = Fq q - R K (as A fragments) and Ob = P Ub (bf16 D tiles); G_L
+  {
+    uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
+      f32x4 d0 = zero4(), d1 = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        if (kk < nk) {
+          const bf16x8 rf = pfragT8(lb, PS_RT, 16 * tb, kk, L);
+          d0 = mfma(pfragT16(lb, PS_K, 32 * kq, kk, L), rf, d0);
+          d1 = mfma(pfragT16(lb, PS_K, 32 * kq + 16, kk, L), rf, d1);
+        }
+      const float fq = F[(PSF_FQ >> 2) + 16 * tb + m];
+      const uint2 c0 = cq[n][0], c1 = cq[n][1];
+      d0[0] = fmaf(fq, __uint_as_float(c0.x << 16), -d0[0]);
+      d0[1] = fmaf(fq, __uint_as_float(c0.x & 0xffff0000u), -d0[1]);
+      d0[2] = fmaf(fq, __uint_as_float(c0.y << 16), -d0[2]);
+      d0[3] = fmaf(fq, __uint_as_float(c0.y & 0xffff0000u), -d0[3]);
+      d1[0] = fmaf(fq, __uint_as_float(c1.x << 16), -d1[0]);
+      d1[1] = fmaf(fq, __uint_as_float(c1.x & 0xffff0000u), -d1[1]);
+      d1[2] = fmaf(fq, __uint_as_float(c1.y << 16), -d1[2]);
+      d1[3] = fmaf(fq, __uint_as_float(c1.y & 0xffff0000u), -d1[3]);
+      gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
+    }
+    uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
+    const int vb = wave;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 y = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        if (kk < tri_kend(tb) / 32) y = mfma(pfragT8(lb, PS_PT, 16 * tb, kk, L), pfrag8(lb, PS_UBT, 16 * vb, kk, L), y);
+      gO[(vb * 4 + tb) * 64 + l] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    }
+    if (tid == 0) *reinterpret_cast<float*>(wsc + WS_GL) = F[(PSF_G >> 2) + CH - 1];
+  }
+  item_barrier();  // the next item's rows overwrite the LDS
+}
+
+// Per-thread constants of the item's row loads: LDS offset of row rr (and rr + 32) at columns c8 .. and
+// the rows' byte offsets in the q, k, v buffers.
+struct PrepRows {
+  int rowoff;
+  uint32_t oq, ok, ov;
+  __device__ __forceinline__ PrepRows(int tid, const RowStrides& rs) {
+    const int rr = tid >> 4, cc = tid & 15;
+    rowoff = rr * 256 + ((cc ^ (rr & 15)) << 4);
+    oq = (uint32_t)rr * 2u * (uint32_t)rs.q + 16u * cc;
+    ok = (uint32_t)rr * 2u * (uint32_t)rs.k + 16u * cc;
+    ov = (uint32_t)rr * 2u * (uint32_t)rs.v + 16u * cc;
+  }
+};
+
 template <typename TG, bool GATE>
 __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -690,10 +749,19 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
     int n_seqs, int n_items, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides rs,
     uint8_t* __restrict__ ws) {
-  __shared__ Prep sm;
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x)
-    prep_item<TG, GATE>(sm, item, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, n_items, T, Hk, Hv,
-                        scale, qk_l2norm, rs, ws);
+  __shared__ PrepShared sm;
+  uint8_t* lb = sm.b;
+  const PrepLane L(lane_id());
+  const PrepRows lr(threadIdx.x, rs);
+  prep_init(lb);
+  RowRegs R;
+  int item = blockIdx.x;
+  if (item < n_items) load_rows(R, item, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
+  for (; item < n_items; item += gridDim.x) {
+    const int next = item + (int)gridDim.x < n_items ? item + (int)gridDim.x : -1;
+    prep_item<TG, GATE>(lb, item, R, next, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, T, Hk, Hv,
+                        scale, qk_l2norm, rs, ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
+  }
 }
 
 // ----------------------------------------------------------------------------------------------- phase 2
@@ -748,14 +816,6 @@ __device__ __forceinline__ int load_flag(const int* f) {
   return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
-// accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. The state pass forms one
-// per chunk in scalar registers, so that its loads and stores take a fixed per-lane offset and no 64-bit vector
-// address arithmetic.
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc raw_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 
 // Stores one O wave's outputs of chunk ci: rows t0 .. t0+3 (D layout) of value column vb * VB + j. Lanes l and
 // l ^ 1 (adjacent columns) swap two values by DPP so that each stores two rows as column pairs, 4-byte words
@@ -1116,7 +1176,7 @@ __global__ void zero_ints_kernel(int* p, int n) {
 }
 
 union FusedShared {
-  Prep p;
+  PrepShared p;
   StateShared s;
 };
 
@@ -1273,21 +1333,37 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
     const int ch = qi + ctl.n_q * m;
     return (chunk0(ch / Hv) + c) * Hv + ch % Hv;
   };
-  for (;;) {
-    __syncthreads();  // every thread has read tk (and the LDS of the last item is free)
-    if (threadIdx.x == 0) {
-      const int u = __hip_atomic_fetch_add(ctl.tickets + 96 * qi + 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      tk = u < n_q_items ? item_of(u) : -1;
+  auto take = [&]() {  // thread 0: the queue's next item (-1: none left)
+    const int u = __hip_atomic_fetch_add(ctl.tickets + 96 * qi + 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return u < n_q_items ? item_of(u) : -1;
+  };
+  // the next ticket is taken as an item starts and its rows load while the item computes (items past a short
+  // chunk table, >= n_items, have no workspace and are passed over)
+  prep_init(sm.p.b);
+  const PrepLane L(lane_id());
+  const PrepRows lr(threadIdx.x, rs);
+  RowRegs R;
+  if (threadIdx.x == 0) tk = take();
+  __syncthreads();
+  int cur = tk;
+  __syncthreads();  // every thread has read tk
+  if (cur >= 0 && cur < n_items) load_rows(R, cur, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
+  while (cur >= 0) {
+    if (threadIdx.x == 0) tk = take();
+    __syncthreads();  // tk visible (and the LDS of the last item is free)
+    const int nxt = tk;
+    const int nload = nxt >= 0 && nxt < n_items ? nxt : -1;
+    if (cur < n_items) {
+      prep_item<TG, GATE>(sm.p.b, cur, R, nload, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, T, Hk, Hv,
+                          scale, qk_l2norm, rs, ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_store(ctl.flags + cur, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      if (nload >= 0) load_rows(R, nload, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
+      __syncthreads();  // every thread has read tk
     }
-    __syncthreads();
-    const int item = tk;
-    if (item < 0) break;
-    if (item >= n_items) continue;  // a chunk past a short chunk table: no workspace (the state job stops before)
-    prep_item<TG, GATE>(sm.p, item, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, n_items, T, Hk, Hv,
-                        scale, qk_l2norm, rs, ws);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(ctl.flags + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    cur = nxt;
   }
 }
 
@@ -1510,27 +1586,22 @@ int launch_form_from_env() {
   return -1;
 }
 std::atomic<int> g_launch_form{launch_form_from_env()};
+
 // Spin bound of the overlapped launch's waits and the never-ready test switch (zgdn_chunk_set_wait_limit).
 std::atomic<int> g_spin_max{SPIN_MAX};
 std::atomic<int> g_never_ready{0};
 
-// Whether an eligible batch takes the overlapped launch: as the launch form says, or (the library's choice)
-// where it measured faster than the two launches on MI355X (same-process comparisons, bf16, dk = dv = 128, us
-// overlapped / two launches): few chains only with long sequences and at most 2 chains a queue (16 chains of
-// 64 chunks 80.7 / 82.8, 8 of 64 56.5 / 56.5; 16 of 32, 16, 8 chunks 51.2 / 45.1, 34.4 / 29.0, 27.6 / 21.1;
-// 32 of 64 -- 4 a queue, whose 32 state workgroups take every CU of the XCD -- 193.2 / 143.4), many chains
-// when there are at least 3072 chunk x head items and 8 chunks or more per chain on average (512 chains of 8
-// chunks 304.8 / 336.1, 256 of 12 233.5 / 252.9, 256 of 16 312.2 / 330.5, 128 of 32 312.4 / 328.7, the
-// 32-sequence packed workload 559.4 / 633.9); 64 chains of 32 lost (166.9 / 148.5), 256 of 8 tied (the state
-// pass starts only after the first items, shares its CUs with phase 1, and with a fixed share of state
-// workgroups short or few chains leave them waiting).
-bool overlap_wanted(bool few, long n_items, double chunks_per_chain, long chains_per_queue) {
-  const int form = g_launch_form.load(std::memory_order_relaxed);
-  if (form == 0) return false;
-  if (form == 1) return true;
-  if (few) return chunks_per_chain >= 64 && chains_per_queue <= 2;
-  return n_items >= 3072 && chunks_per_chain >= 8;
-}
+// Whether an eligible batch takes the overlapped launch: only when the launch form asks for it. With the
+// phase-1 item of this file the two launches measured faster on every shape tried (MI355X, bf16,
+// dk = dv = 128, HIP graph replay, us two launches / overlapped, both forms forced in one process):
+// 1 x 4096 at 16 heads 81.3 / 86.4, at 8 heads 57.3 / 57.7; 2 x 4096 139.6 / 168.0; 1 x 2048 47.2 / 56.3;
+// 4 x 1024 63.9 / 81.7; packed 32 x 512, 16 x 1024, 8 x 2048 310.2 / 347.3, 303.6 / 312.7, 302.6 / 311.8;
+// 32 packed sequences of 64 .. 2048 tokens 730.0 / 747.7. (The overlapped launch won where phase 1 was slower:
+// with an item of 10-11k VALU instructions it took the 4096-token, 16-head prefill in 78-81 us against 83 us,
+// and the 32-sequence packed batch in 548-559 against 624-634 us.) The overlapped state jobs share their CUs
+// with phase-1 workgroups, which slows their chunk steps by a third, and the faster phase 1 leaves less of its
+// time to hide.
+bool overlap_wanted(bool, long, double, long) { return g_launch_form.load(std::memory_order_relaxed) == 1; }
 
 int device_cus() {
   int dev = 0, n_cu = 256;
