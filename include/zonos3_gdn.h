@@ -64,6 +64,15 @@ int zgdn_recurrent_fwd(const void* q, const void* k, const void* v, int qkv_dtyp
 size_t zgdn_chunk_workspace_size(int n_chunks, int Hv);
 
 /*
+ * Bytes of workspace zgdn_chunk_fwd needs for n_chunks chunks and Hv value heads at head sizes K == V and element
+ * type qkv_dtype of q/k/v: zgdn_chunk_workspace_size's for bf16 at K == V == 128; 164,096 bytes (K == 128) or
+ * 82,176 bytes (K == 64) per chunk and head on the fp32-arithmetic path (fp32 q/k/v, or K == 64); 0 for a
+ * combination zgdn_chunk_fwd does not take. The library's own function, sizing FLA's internal intermediates
+ * (chunk_gated_delta_rule_fwd allocates them itself).
+ */
+size_t zgdn_chunk_workspace_bytes(int n_chunks, int Hv, int K, int V, int qkv_dtype);
+
+/*
  * Launch form of zgdn_chunk_fwd for this process: -1 the library's choice (two launches, above), 0 always
  * phase 1 and the state pass as two launches, 1 the overlapped launch for every eligible batch. The initial value is read once,
  * when the library is loaded, from the environment variable ZGDN_CHUNK_OVERLAP ("0" or "1"; otherwise -1); no
@@ -123,13 +132,15 @@ int zgdn_chunk_set_wait_limit(int spins, int never_ready);
 size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv);
 
 /*
- * Chunked (WY/UT form, 64-token chunks) gated delta rule over whole sequences on bf16 MFMA with fp32
- * accumulation: the prefill core. Replaces FLA's chunk_gated_delta_rule_fwd as called at
- * servers/sgl/src/zonos3_sgl/models/gdn.py:418-434 (state_v_first=True, chunk_size=64, output o and the
- * final state), itself the chunked form of model/src/zonos3/reference/lm.py:574-583.
- *   q, k, v: bf16, K == V == 128, rows of [B * T] tokens q_ld / k_ld / v_ld elements apart (a token's heads
- *   contiguous; a multiple of 8 elements, bases 16-byte aligned), so that q, k, v may be column slices of one
- *   wider row such as the conv output. o: bf16 [B, T, Hv, V] (dense).
+ * Chunked (WY/UT form, 64-token chunks) gated delta rule over whole sequences: the prefill core. Replaces FLA's
+ * chunk_gated_delta_rule_fwd as called at servers/sgl/src/zonos3_sgl/models/gdn.py:418-434 (state_v_first=True,
+ * chunk_size=64, output o and the final state), itself the chunked form of
+ * model/src/zonos3/reference/lm.py:574-583, in the layer's dtype (lm.py:556-602 runs fp32 or bf16).
+ *   q, k, v: element type qkv_dtype (BF16 or F32), K == V, 64 or 128. bf16 at 128 runs on bf16 MFMA with fp32
+ *   accumulation (bf16 operands; hi + lo pairs where the state needs them); fp32 inputs, and bf16 at 64, run in
+ *   fp32 arithmetic (v_mfma_f32_16x16x4_f32). Rows of [B * T] tokens q_ld / k_ld / v_ld elements apart (a
+ *   token's heads contiguous; a multiple of 16 bytes of elements, bases 16-byte aligned), so that q, k, v may be
+ *   column slices of one wider row such as the conv output. o: qkv_dtype [B, T, Hv, V] (dense).
  *   g, beta: gb_dtype, rows of Hv values gb_ld elements apart (column slices of the input projection read in
  *   place). With A_log and dt_bias (float32 [Hv], both or neither) g holds the raw gate input a and the log
  *   decay is -exp(A_log[h]) * softplus(a + dt_bias[h]) (FLA use_gate_in_kernel=True, gdn.py:430-432);
@@ -140,8 +151,8 @@ size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv);
  *   cu_seqlens [n_seqs+1] + chunk_indices [n_chunks, 2] (sequence, chunk within it; the table of
  *   gdn.py:49-59) for packed sequences (B == 1); otherwise n_chunks is derived from B and T.
  *   initial_state NULL = zeros; final_state NULL = not written; may equal initial_state (in place).
- *   workspace: device memory of at least zgdn_chunk_workspace_size(n_chunks, Hv) bytes (plus
- *   zgdn_chunk_segment_workspace_size(B, T, Hv) for the segmented pass of unpacked batches).
+ *   workspace: device memory of at least zgdn_chunk_workspace_bytes(n_chunks, Hv, K, V, qkv_dtype) bytes (plus,
+ *   on the bf16 path, zgdn_chunk_segment_workspace_size(B, T, Hv) for the segmented pass of unpacked batches).
  */
 int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, const void* g, const void* beta,
                    int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
@@ -158,8 +169,9 @@ int zgdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, c
  * segmented state pass of long unpacked prompts is taken only when its extra space fits the scratch as well,
  * else the plain pass, whose results differ from the segmented one's in the last bits (its combine rounds
  * through bf16 hi / lo parts). The caller still passes every input and output. The workspace is the
- * library's own per-device scratch of zgdn_chunk_noalloc_max_bytes() bytes (64 MiB: 680 chunk x head items,
- * e.g. 4 heads up to 10,880 tokens or 16 heads up to 2,720), a static device array held by each device the
+ * library's own per-device scratch of zgdn_chunk_noalloc_max_bytes() bytes (64 MiB; on the bf16 path 680 chunk x
+ * head items, e.g. 4 heads up to 10,880 tokens or 16 heads up to 2,720; 408 items on the fp32 path at K == 128,
+ * 816 at K == 64: zgdn_chunk_workspace_bytes sizes them), a static device array held by each device the
  * library runs on until the process ends; calls needing more fail with ZGDN_EINVAL before any launch. Its
  * address is looked up once per device (hipGetSymbolAddress, with the device current), then no call
  * allocates. Every call on one device shares that device's scratch, which keeps the last call's contents (the

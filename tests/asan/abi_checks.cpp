@@ -76,6 +76,13 @@ int main() {
     ++failures;
     std::fprintf(stderr, "FAIL chunk workspace size\n");
   }
+  if (zgdn_chunk_workspace_bytes(4, 4, 96, 96, 0) != 0 || zgdn_chunk_workspace_bytes(4, 4, 64, 64, 0) == 0) {
+    ++failures;
+    std::fprintf(stderr, "FAIL chunk workspace bytes\n");
+  }
+  expect("chunk fp32 strides", zgdn_chunk_fwd(p, p, p, 0, p, p, 1, nullptr, nullptr, 1, f, f, p, nullptr, nullptr, 0, 1,
+                                              1, 64, 4, 4, 64, 64, 258, 256, 256, 4, 0, 0.1f, p, 1 << 30, nullptr),
+         ZGDN_EINVAL, "multiples of 4");
   expect("launch form", zgdn_chunk_set_launch_form(7), ZGDN_EINVAL, nullptr);
   expect("launch form default", zgdn_chunk_set_launch_form(-1), ZGDN_OK, nullptr);
   expect("chunk status null", zgdn_chunk_status(nullptr, 0), ZGDN_EINVAL, nullptr);

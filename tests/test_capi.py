@@ -27,7 +27,7 @@ def test_header_declares_entry_points():
             "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size", "zgdn_chunk_set_launch_form",
             "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit",
             "zgdn_chunk_status_async", "zgdn_chunk_overlap_queues",
-            "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc"} == _declared()
+            "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc", "zgdn_chunk_workspace_bytes"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -94,10 +94,26 @@ def test_bad_arguments_fail_with_a_message(gdn):
     chunk[23], chunk[26] = 128, 0  # g/beta rows narrower than the heads
     assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"row strides" in lib.zgdn_last_error()
     chunk[26] = 1
-    chunk[21] = 64  # K
-    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=64" in lib.zgdn_last_error()
-    chunk[21], chunk[3] = 128, 0  # fp32 q/k/v
-    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"bf16" in lib.zgdn_last_error()
+    chunk[21] = 96  # K
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=96" in lib.zgdn_last_error()
+    chunk[21], chunk[22] = 64, 128  # K != V
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EUNSUPPORTED and b"K=64 V=128" in lib.zgdn_last_error()
+    chunk[21], chunk[3] = 128, 5  # q/k/v dtype code
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"dtype code 5" in lib.zgdn_last_error()
+    # fp32 q/k/v (and 64-wide heads) take the fp32-arithmetic path: its workspace, its row-stride multiple
+    chunk[3] = 0
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"workspace" in lib.zgdn_last_error()
+    chunk[23] = 1536 + 4  # a multiple of 4 fp32 elements: accepted by the stride check (then the workspace)
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"workspace" in lib.zgdn_last_error()
+    chunk[23] = 1536 + 2
+    assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"multiples of 4" in lib.zgdn_last_error()
+    chunk[23], chunk[3] = 128, 1
+    # per-dtype workspace: the bf16 path's at 128; 5 fp32 blocks of 64 x D + 256 bytes an item otherwise
+    wb = lib.zgdn_chunk_workspace_bytes
+    assert wb(64, 16, 128, 128, 1) == lib.zgdn_chunk_workspace_size(64, 16)
+    assert wb(64, 16, 128, 128, 0) == 64 * 16 * (5 * 64 * 128 * 4 + 256) == 64 * 16 * 164096
+    assert wb(4, 4, 64, 64, 0) == wb(4, 4, 64, 64, 1) == 16 * (5 * 64 * 64 * 4 + 256) == 16 * 82176
+    assert wb(4, 4, 96, 96, 0) == 0 and wb(4, 4, 64, 128, 1) == 0 and wb(4, 4, 128, 128, 3) == 0
     # items, then the control block of the overlapped launch (45 x 256 bytes: tickets, per-CU arrival counts;
     # then one 4-byte flag per item)
     assert lib.zgdn_chunk_workspace_size(64, 16) == 64 * 16 * 98560 + 256 * 45 + 64 * 16 * 4

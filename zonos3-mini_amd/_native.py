@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
          c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     ),
     "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
+    "zgdn_chunk_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "zgdn_chunk_set_launch_form": (c_int, [c_int]),
     "zgdn_chunk_get_launch_form": (c_int, []),
     "zgdn_chunk_status": (c_int, [POINTER(c_int), c_int]),

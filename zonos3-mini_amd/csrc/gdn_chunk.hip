@@ -99,38 +99,6 @@ __device__ __forceinline__ uint4 kappa_frag(f32x4 d0, f32x4 d1) {
                     pack_bf16x2(d1[2], d1[3]));
 }
 
-// Token range of chunk `c`: packed sequences (cu != nullptr, chunk index table (seq, j)) or B x T batches.
-struct ChunkRange {
-  int t0, len;
-};
-__device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, const int32_t* chunk_idx, int T,
-                                                  int n_seqs) {
-  ChunkRange r;
-  if (cu != nullptr) {
-    const int s = chunk_idx[2 * c], j = chunk_idx[2 * c + 1];
-    if (s < 0 || s >= n_seqs || j < 0) {  // a malformed table row reads nothing
-      r.t0 = 0;
-      r.len = 0;
-      return r;
-    }
-    int bos, eos;
-    seq_bounds(cu, s, T, bos, eos);
-    if (j >= (eos - bos + CH - 1) / CH) {  // past the sequence's chunks
-      r.t0 = 0;
-      r.len = 0;
-      return r;
-    }
-    r.t0 = bos + j * CH;
-    r.len = min(CH, eos - r.t0);
-  } else {
-    const int nt = (T + CH - 1) / CH;
-    const int b = c / nt, j = c % nt;
-    r.t0 = b * T + j * CH;
-    r.len = min(CH, T - j * CH);
-  }
-  return r;
-}
-
 // Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
 // accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. The state pass forms one
 // per chunk in scalar registers, so that its loads and stores take a fixed per-lane offset and no 64-bit vector
@@ -164,13 +132,6 @@ __device__ __forceinline__ void lower_tile(int t, int& rb, int& cb) {
 // Contraction length over tokens for token tile tb of a lower-triangular left operand.
 __device__ __forceinline__ int tri_kend(int tb) { return tb < 2 ? 32 : 64; }
 
-// Elements between consecutive tokens of q, k, v and of g / beta (a token's heads are contiguous in each), so
-// that the kernel reads column slices of wider rows (the conv output, the input projection) in place;
-// beta_sigmoid: beta holds the raw input b and the kernel takes sigmoid(b) (in fp32).
-struct RowStrides {
-  long q, k, v, gb;
-  int beta_sigmoid;
-};
 
 // ----------------------------------------------------------------------------------------------- phase 1
 //
@@ -1692,6 +1653,13 @@ extern "C" size_t zgdn_chunk_workspace_size(int n_chunks, int Hv) {
   return items * zgdn::WS_CHUNK + zgdn::fused_ctl_bytes((int)items);
 }
 
+extern "C" size_t zgdn_chunk_workspace_bytes(int n_chunks, int Hv, int K, int V, int qkv_dtype) {
+  if (K != V || (K != 64 && K != 128) || (qkv_dtype != ZGDN_F32 && qkv_dtype != ZGDN_BF16)) return 0;
+  if (qkv_dtype == ZGDN_BF16 && K == zgdn::DK) return zgdn_chunk_workspace_size(n_chunks, Hv);
+  const size_t items = (size_t)(n_chunks > 0 ? n_chunks : 0) * (size_t)(Hv > 0 ? Hv : 0);
+  return items * zgdn::chunk32_item_bytes(K);
+}
+
 extern "C" size_t zgdn_chunk_segment_workspace_size(int B, int T, int Hv) {
   using namespace zgdn;
   if (B < 1 || T < 1 || Hv < 1) return 0;
@@ -1710,19 +1678,24 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
   // (with no tokens, T == 0, the token arrays may be empty allocations: only the states are touched)
   if (!workspace || (T > 0 && (!q || !k || !v || !g || !beta || !o)))
     return fail(ZGDN_EINVAL, "%s: null pointer", fn);
-  if (K != DK || V != DV) return fail(ZGDN_EUNSUPPORTED, "%s: K=%d V=%d (supported: 128, 128)", fn, K, V);
-  if (qkv_dtype != ZGDN_BF16) return fail(ZGDN_EUNSUPPORTED, "%s: q/k/v must be bf16", fn);
+  if (qkv_dtype != ZGDN_F32 && qkv_dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, qkv_dtype);
+  if (K != V || (K != 64 && K != 128))
+    return fail(ZGDN_EUNSUPPORTED, "%s: K=%d V=%d (supported: K == V, 64 or 128)", fn, K, V);
+  // bf16 q/k/v with 128-wide heads run on bf16 MFMA (this file); fp32 inputs and 64-wide heads on the
+  // fp32-arithmetic path (gdn_chunk_f32.hip)
+  const bool bf16_path = qkv_dtype == ZGDN_BF16 && K == DK;
   if (gb_dtype != ZGDN_F32 && gb_dtype != ZGDN_BF16) return fail(ZGDN_EINVAL, "%s: dtype code %d", fn, gb_dtype);
   if (B < 1 || T < 0 || Hk < 1 || Hv < 1 || Hv % Hk)
     return fail(ZGDN_EINVAL, "%s: bad sizes B=%d T=%d Hk=%d Hv=%d", fn, B, T, Hk, Hv);
   if ((A_log == nullptr) != (dt_bias == nullptr))
     return fail(ZGDN_EINVAL, "%s: A_log and dt_bias go together", fn);
-  // row strides: at least a token's heads; q / k / v rows start on 16-byte boundaries (the kernel reads
-  // 8-element groups)
-  if (q_ld < (long)Hk * K || k_ld < (long)Hk * K || v_ld < (long)Hv * V || gb_ld < Hv || q_ld % 8 || k_ld % 8 ||
-      v_ld % 8 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16)
+  // row strides: at least a token's heads; q / k / v rows start on 16-byte boundaries (the kernels read
+  // 16-byte groups: 8 bf16 or 4 fp32 elements)
+  const long ve = qkv_dtype == ZGDN_F32 ? 4 : 8;
+  if (q_ld < (long)Hk * K || k_ld < (long)Hk * K || v_ld < (long)Hv * V || gb_ld < Hv || q_ld % ve ||
+      k_ld % ve || v_ld % ve || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16)
     return fail(ZGDN_EINVAL, "%s: row strides q=%ld k=%ld v=%ld g/beta=%ld (need >= a token's heads, q/k/v "
-                "multiples of 8 elements from 16-byte aligned bases)", fn, q_ld, k_ld, v_ld, gb_ld);
+                "multiples of %ld elements from 16-byte aligned bases)", fn, q_ld, k_ld, v_ld, gb_ld, ve);
   const RowStrides rs{q_ld, k_ld, v_ld, gb_ld, beta_sigmoid != 0};
   int N = B;
   if (cu_seqlens != nullptr) {
@@ -1733,10 +1706,13 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
     n_chunks = B * ((T + CH - 1) / CH);
   }
   if (n_chunks < 0) return fail(ZGDN_EINVAL, "%s: n_chunks=%d", fn, n_chunks);
-  if (workspace_bytes < zgdn_chunk_workspace_size(n_chunks, Hv))
-    return fail(ZGDN_EINVAL, "%s: workspace of %zu bytes, need %zu", fn, workspace_bytes,
-                zgdn_chunk_workspace_size(n_chunks, Hv));
+  const size_t need = zgdn_chunk_workspace_bytes(n_chunks, Hv, K, V, qkv_dtype);
+  if (workspace_bytes < need)
+    return fail(ZGDN_EINVAL, "%s: workspace of %zu bytes, need %zu", fn, workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
+  if (!bf16_path)
+    return chunk32_fwd(fn, q, k, v, qkv_dtype, g, beta, gb_dtype, A_log, dt_bias, qk_l2norm, initial_state,
+                       final_state, o, cu_seqlens, chunk_indices, N, n_chunks, T, Hk, Hv, K, scale, rs, workspace, s);
   uint8_t* ws = (uint8_t*)workspace;
   const bool gate = A_log != nullptr;
   // phase 2: plain runs, or (unpacked batches that would hold few CUs, workspace permitting) segmented runs
@@ -1871,7 +1847,7 @@ extern "C" int zgdn_chunk_fwd_noalloc(const void* q, const void* k, const void* 
   const char* fn = "zgdn_chunk_fwd_noalloc";
   const int nc = cu_seqlens != nullptr ? n_chunks : (B > 0 && T >= 0 ? B * ((T + CH - 1) / CH) : 0);
   if (nc < 0 || Hv < 1) return fail(ZGDN_EINVAL, "%s: n_chunks=%d Hv=%d", fn, nc, Hv);
-  const size_t need = zgdn_chunk_workspace_size(nc, Hv);
+  const size_t need = zgdn_chunk_workspace_bytes(nc, Hv, K, V, qkv_dtype);  // 0: unsupported, refused below
   if (need > NOALLOC_SCRATCH_BYTES)
     return fail(ZGDN_EINVAL, "%s: %d chunks x %d heads need %zu bytes of workspace, above the %zu-byte scratch "
                 "of this entry point (use zgdn_chunk_fwd with a caller workspace)", fn, nc, Hv, need,
@@ -1881,7 +1857,7 @@ extern "C" int zgdn_chunk_fwd_noalloc(const void* q, const void* k, const void* 
   if (st != ZGDN_OK) return st;
   // the segmented state pass's extra space when it fits the scratch as well, else the plain pass
   size_t bytes = need;
-  if (cu_seqlens == nullptr && B > 0 && T > 0) {
+  if (cu_seqlens == nullptr && B > 0 && T > 0 && qkv_dtype == ZGDN_BF16 && K == DK) {
     const size_t seg = zgdn_chunk_segment_workspace_size(B, T, Hv);
     if (seg > 0 && need + seg <= NOALLOC_SCRATCH_BYTES) bytes = need + seg;
   }

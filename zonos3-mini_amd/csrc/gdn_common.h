@@ -117,6 +117,70 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int T, int&
   eos = min(max(cu[s + 1], bos), T);
 }
 
+// ------------------------------------------------------------------------------------------ chunked prefill
+
+constexpr int CHUNK_LEN = 64;  // tokens per chunk of the chunked (WY / UT form) prefill
+
+// Token range of chunk `c`: packed sequences (cu != nullptr, chunk index table (seq, j)) or B x T batches.
+struct ChunkRange {
+  int t0, len;
+};
+__device__ __forceinline__ ChunkRange chunk_range(int c, const int32_t* cu, const int32_t* chunk_idx, int T,
+                                                  int n_seqs) {
+  ChunkRange r;
+  if (cu != nullptr) {
+    const int s = chunk_idx[2 * c], j = chunk_idx[2 * c + 1];
+    if (s < 0 || s >= n_seqs || j < 0) {  // a malformed table row reads nothing
+      r.t0 = 0;
+      r.len = 0;
+      return r;
+    }
+    int bos, eos;
+    seq_bounds(cu, s, T, bos, eos);
+    if (j >= (eos - bos + CHUNK_LEN - 1) / CHUNK_LEN) {  // past the sequence's chunks
+      r.t0 = 0;
+      r.len = 0;
+      return r;
+    }
+    r.t0 = bos + j * CHUNK_LEN;
+    r.len = min(CHUNK_LEN, eos - r.t0);
+  } else {
+    const int nt = (T + CHUNK_LEN - 1) / CHUNK_LEN;
+    const int b = c / nt, j = c % nt;
+    r.t0 = b * T + j * CHUNK_LEN;
+    r.len = min(CHUNK_LEN, T - j * CHUNK_LEN);
+  }
+  return r;
+}
+
+// First chunk (in the canonical table order: sequence by sequence, chunk by chunk) and token range of packed
+// sequence `seq` (cu != nullptr), or of batch row `seq` of an unpacked B x T batch.
+__device__ __forceinline__ void seq_chunks(const int32_t* cu, int seq, int T, int& c0, int& bos, int& len) {
+  if (cu != nullptr) {
+    int eos;
+    seq_bounds(cu, seq, T, bos, eos);
+    len = eos - bos;
+    c0 = 0;
+    for (int s = 0; s < seq; ++s) {
+      int sb, se;
+      seq_bounds(cu, s, T, sb, se);
+      c0 += (se - sb + CHUNK_LEN - 1) / CHUNK_LEN;
+    }
+  } else {
+    bos = seq * T;
+    len = T;
+    c0 = seq * ((T + CHUNK_LEN - 1) / CHUNK_LEN);
+  }
+}
+
+// Elements between consecutive tokens of q, k, v and of g / beta (a token's heads are contiguous in each), so
+// that the kernel reads column slices of wider rows (the conv output, the input projection) in place;
+// beta_sigmoid: beta holds the raw input b and the kernel takes sigmoid(b) (in fp32).
+struct RowStrides {
+  long q, k, v, gb;
+  int beta_sigmoid;
+};
+
 // -------------------------------------------------------------------------------------------------- math
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
@@ -134,4 +198,13 @@ namespace zgdn {
 // Records a message for zgdn_last_error() and returns `code`.
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// The fp32-arithmetic chunked path (gdn_chunk_f32.hip): workspace bytes per (chunk, value head) item at head
+// size D, and the forward behind zgdn_chunk_fwd for fp32 q/k/v and for 64-wide heads (arguments checked there).
+size_t chunk32_item_bytes(int D);
+int chunk32_fwd(const char* fn, const void* q, const void* k, const void* v, int qkv_dtype, const void* g,
+                const void* beta, int gb_dtype, const float* A_log, const float* dt_bias, int qk_l2norm,
+                const float* s_in, float* s_out, void* o, const int32_t* cu, const int32_t* chunk_idx, int N,
+                int n_chunks, int T, int Hk, int Hv, int D, float scale, const RowStrides& rs, void* workspace,
+                hipStream_t s);
 }  // namespace zgdn

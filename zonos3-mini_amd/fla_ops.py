@@ -64,7 +64,7 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale=None, initial_state=None,
     """Gated delta rule over packed sequences (gdn.py:418-434). Returns a 6-tuple whose [1] is o
     [B, T, Hv, V] (q's dtype) and [3] the final state [N, Hv, V, K] float32 (value-major).
 
-    bf16 inputs with K == V == 128 run the chunked kernel; other dtypes / head sizes the recurrent one."""
+    bf16 or fp32 inputs with K == V of 64 or 128 run the chunked kernels; other head sizes the recurrent one."""
     if unsupported:
         raise RuntimeError(f"chunk_gated_delta_rule_fwd: unsupported arguments {sorted(unsupported)}")
     if not state_v_first:
@@ -79,7 +79,8 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale=None, initial_state=None,
         initial_state = initial_state.float()
     kw = dict(scale=scale, initial_state=initial_state, output_final_state=output_final_state,
               cu_seqlens=cu_seqlens, A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=use_qk_l2norm_in_kernel)
-    chunked = q.dtype == torch.bfloat16 and q.shape[-1] == 128 and v.shape[-1] == 128
+    chunked = (q.dtype in (torch.bfloat16, torch.float32) and q.shape[-1] == v.shape[-1]
+               and q.shape[-1] in (64, 128))
     if chunked:
         o, final = ops.chunk_fwd(q, k, v, g, beta, chunk_indices=chunk_indices, **kw)
     else:

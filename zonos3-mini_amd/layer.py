@@ -10,8 +10,9 @@ runs the projections through ``self._lin`` (so accent adapters still apply), rep
 or ``Zonos3LM._gdn = gdn`` (the class).
 
 Data path: one row (decode) -> the fused decode-block kernel (conv, SiLU, L2, gate, update, gated norm in
-one launch); more rows -> the conv kernel, then the chunked kernel (bf16) or the recurrent kernel (fp32),
-both with the q/k L2-norm and the gate formed in the kernel, then the gated-RMSNorm kernel.
+one launch); more rows -> the conv kernel, then the chunked kernels (bf16 MFMA for bf16 at head size 128, fp32
+arithmetic for fp32 and for 64-wide heads; the recurrent kernel for other head sizes), with the q/k L2-norm and
+the gate formed in the kernel, then the gated-RMSNorm kernel.
 """
 
 from __future__ import annotations
@@ -74,7 +75,7 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
     q, k, v = (part.unflatten(-1, (heads, hd)) for part in conv.split(inner, -1))
     s0 = None if state is None else state.reshape(1, heads, hd, hd).float().contiguous()
     kw = dict(initial_state=s0, A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=True)
-    if dt == torch.bfloat16 and hd == 128:
+    if dt in (torch.bfloat16, torch.float32) and hd in (64, 128):
         o, new_state = ops.chunk_fwd(q, k, v, aa.unsqueeze(0), b.unsqueeze(0), beta_is_logit=True, **kw)
         beta = None
     else:

@@ -319,22 +319,24 @@ VALIDATE = os.environ.get("ZGDN_VALIDATE", "0") not in ("", "0")
 def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
               chunk_indices=None, A_log=None, dt_bias=None, final_state=None, use_qk_l2norm=False,
               beta_is_logit=False):
-    """Chunked gated delta rule (64-token chunks, bf16 MFMA, fp32 state): the prefill core.
+    """Chunked gated delta rule (64-token chunks, fp32 state): the prefill core.
 
     The operator behind FLA's ``chunk_gated_delta_rule_fwd`` as the serving layer calls it
-    (``servers/sgl/src/zonos3_sgl/models/gdn.py:418-434``): q, k [B, T, Hk, 128], v [B, T, Hv, 128] bf16;
-    g, beta [B, T, Hv] float32 or bfloat16. With ``A_log``/``dt_bias`` (float32 [Hv]) g is the raw gate input
+    (``servers/sgl/src/zonos3_sgl/models/gdn.py:418-434``), in the layer's dtype (``lm.py:556-602``): q, k
+    [B, T, Hk, K], v [B, T, Hv, V] with K == V of 64 or 128, all bfloat16 or all float32 (bf16 at 128 runs on
+    bf16 MFMA; fp32, and 64-wide heads, in fp32 arithmetic); g, beta [B, T, Hv] float32 or bfloat16. With ``A_log``/``dt_bias`` (float32 [Hv]) g is the raw gate input
     and the decay is formed in the kernel (``use_gate_in_kernel=True``). ``use_qk_l2norm``: q, k are the raw
     rows, L2-normalised in the kernel with fp32 factors (never rounded after the norm). ``beta_is_logit``: beta
     holds the raw input b and the kernel takes sigmoid(b) in fp32 (what ``sigmoid`` returns, FLA's
     fused_beta_sigmoid_fwd at gdn.py:423). Packed sequences: B == 1, ``cu_seqlens`` int32 [N+1] and optionally
     ``chunk_indices`` int32 [n_chunks, 2]. q, k, v, g, beta may be column slices of wider rows (the conv output,
     the input projection): rows whose stride the kernel can take are read in place, others are copied first.
-    Returns (o [B, T, Hv, 128] bf16, final state [N, Hv, 128, 128] float32 or None)."""
+    Returns (o [B, T, Hv, V] in q's dtype, final state [N, Hv, V, K] float32 or None)."""
     dev = q.device if isinstance(q, torch.Tensor) else None
-    q, q_ld = _rows_in_place("q", q, 2, dev, 8, 16)
-    k, k_ld = _rows_in_place("k", k, 2, dev, 8, 16)
-    v, v_ld = _rows_in_place("v", v, 2, dev, 8, 16)
+    ve = 4 if isinstance(q, torch.Tensor) and q.dtype == torch.float32 else 8  # elements in 16 bytes
+    q, q_ld = _rows_in_place("q", q, 2, dev, ve, 16)
+    k, k_ld = _rows_in_place("k", k, 2, dev, ve, 16)
+    v, v_ld = _rows_in_place("v", v, 2, dev, ve, 16)
     _require(q.dim() == 4 and k.shape == q.shape, f"q, k: expected equal [B, T, Hk, K], got {tuple(q.shape)}, "
                                                   f"{tuple(k.shape)}")
     B, T, Hk, K = q.shape
@@ -345,9 +347,11 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     if beta_ld != gb_ld:  # one row stride serves both
         g, gb_ld = g.contiguous(), Hv
         beta = beta.contiguous()
-    _require(K == 128 and V == 128, f"chunk_fwd: head dims K={K}, V={V}; the chunked kernel needs 128")
+    _require(K == V and K in (64, 128), f"chunk_fwd: head dims K={K}, V={V}; the chunked kernels take K == V, "
+                                         f"64 or 128")
     _require(Hv % Hk == 0, f"value heads ({Hv}) must be a multiple of key heads ({Hk})")
-    _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "chunk_fwd: q, k, v must be bfloat16")
+    _require(q.dtype == k.dtype == v.dtype and q.dtype in (torch.bfloat16, torch.float32),
+             "chunk_fwd: q, k, v must all be bfloat16 or all float32")
     _require(g.shape == (B, T, Hv) and beta.shape == (B, T, Hv), f"g, beta: expected [{B}, {T}, {Hv}]")
     _require(g.dtype == beta.dtype, "g, beta: must share a dtype")
     gb_code = _code(g, "g")
@@ -377,14 +381,15 @@ def chunk_fwd(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
                  f"final_state: expected float32 [{n_seqs}, {Hv}, {V}, {K}]")
     elif output_final_state:
         final_state = torch.empty(n_seqs, Hv, V, K, device=dev, dtype=torch.float32)
-    o = torch.empty(B, T, Hv, V, device=dev, dtype=torch.bfloat16)
-    ws_bytes = int(_native.lib().zgdn_chunk_workspace_size(n_chunks, Hv))
-    if cu_seqlens is None:  # room for the segmented state pass when the library would take it
+    o = torch.empty(B, T, Hv, V, device=dev, dtype=q.dtype)
+    qkv_code = _code(q, "q")
+    ws_bytes = int(_native.lib().zgdn_chunk_workspace_bytes(n_chunks, Hv, K, V, qkv_code))
+    if cu_seqlens is None and qkv_code == BF16 and K == 128:  # room for the segmented state pass when taken
         ws_bytes += int(_native.lib().zgdn_chunk_segment_workspace_size(B, T, Hv))
     workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     scale = K**-0.5 if scale is None else float(scale)
     _native.call(
-        "zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), BF16, g.data_ptr(), beta.data_ptr(), gb_code,
+        "zgdn_chunk_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), qkv_code, g.data_ptr(), beta.data_ptr(), gb_code,
         _ptr(A_log), _ptr(dt_bias), int(bool(use_qk_l2norm)), _ptr(initial_state), _ptr(final_state), o.data_ptr(),
         _ptr(cu_seqlens),
         _ptr(chunk_indices), n_seqs, n_chunks, B, T, Hk, Hv, K, V, q_ld, k_ld, v_ld, gb_ld, int(bool(beta_is_logit)),
