@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "GDN tokens/s (decode B=64, prefill T=4096) + % of HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 matrix (v_mfma_f32_*_f32) peak of MI355X
 
 DECODE = dict(B=64, H=16, K=128, V=128)
 DECODE_BYTES_PER_TOKEN_HEAD = 2 * 128 * 128 * 4 + 2 * (128 + 128) * 2 + 2 * 4  # 132,104
@@ -51,7 +52,8 @@ def _args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    p.add_argument("--only", choices=["decode", "prefill", "varlen", "fused", "serving", "attnres", "layer", "accent"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "prefill_f32", "varlen", "fused", "serving", "attnres", "layer",
+                                      "accent"], default=None,
                    help="run one workload only (profiling runs); the JSON line then carries that workload")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 64 MiB device copy 10 times (the scale for HBM byte counters)")
@@ -167,6 +169,46 @@ def bench_prefill(torch, gdn, reps=50):
             "algorithmic_flops": int(flops),
         },
     }
+
+
+def bench_prefill_f32(torch, gdn, reps=20):
+    """The chunked prefill in fp32 (the layer's fp32 dtype, lm.py:556-602): the prefill workload's shape with
+    fp32 q/k/v/o (T=4096, H=16, d=128), and the CPU-oracle configuration (B=1, T=256, H=4, d=64, fp32) with
+    its CPU time beside it. fp32 arithmetic throughout, so the roofline is the fp32 matrix peak."""
+    from oracle import gdn_oracle as O
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(dev)
+    out = {}
+    for name, (B, T, H, D, seed) in (("T4096_H16_d128", (1, 4096, 16, 128, 1003)),
+                                     ("T256_H4_d64", (1, 256, 4, 64, 1001))):
+        d = O.make_inputs(B, T, H, H, D, D, seed=seed)
+        x = {n: d[n].to(dev) for n in ("q", "k", "v", "g", "beta")}
+
+        def run():
+            return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
+
+        ms = kernel_ms(torch, stream, run, reps)
+        flops = (2 * _C * _C * 5 * D + 6 * _C * D * D + _C**3 / 3) * (-(-T // _C)) * H * B
+        tflops = flops / (ms * 1e-3) / 1e12
+        out[name] = {
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "ms": round(ms, 5),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                         "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": int(flops)},
+        }
+        if name == "T256_H4_d64":
+            def cpu():
+                O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+
+            threads = _host_threads()
+            sec = _cpu_median(torch, cpu, threads)
+            out[name]["cpu_baseline"] = {"value": round(B * T / sec, 1), "unit": "tokens/s", "cores": threads,
+                                         "kind": "port", "sample": "the whole configuration through the torch CPU "
+                                         "restatement of the reference token loop, median of 5 runs after 1 warm-up"}
+    return {"workload": "chunked prefill in fp32: q/k/v/o fp32, fp32 state, zero initial state, chunk 64 (phase 1 "
+                        "and the state pass in fp32 arithmetic on v_mfma_f32_16x16x4_f32)", **out}
 
 
 VARLEN = dict(n_seqs=32, lo=64, hi=2048, H=16, K=128, V=128)
@@ -592,8 +634,9 @@ def main():
     gdn = importlib.import_module("zonos3-mini_amd")
     if a.calibrate_copy:
         calibrate_copy(torch)
-    if a.only in ("prefill", "varlen", "fused"):
-        fn = {"prefill": bench_prefill, "varlen": bench_varlen, "fused": bench_fused}[a.only]
+    if a.only in ("prefill", "prefill_f32", "varlen", "fused"):
+        fn = {"prefill": bench_prefill, "prefill_f32": bench_prefill_f32, "varlen": bench_varlen,
+              "fused": bench_fused}[a.only]
         print(json.dumps({"workload_only": a.only, **fn(torch, gdn)}), flush=True)
         return
     if a.only == "serving":
@@ -645,6 +688,7 @@ def main():
         print(json.dumps(line), flush=True)
         return
     line["prefill"] = bench_prefill(torch, gdn)
+    line["prefill_f32"] = bench_prefill_f32(torch, gdn)
     line["varlen_prefill"] = bench_varlen(torch, gdn)
     line["fused_decode_block"] = bench_fused(torch, gdn)
     line["serving_decode"] = bench_serving(torch)

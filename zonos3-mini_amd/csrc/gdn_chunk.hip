@@ -99,14 +99,6 @@ __device__ __forceinline__ uint4 kappa_frag(f32x4 d0, f32x4 d1) {
                     pack_bf16x2(d1[2], d1[3]));
 }
 
-// Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
-// accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. The state pass forms one
-// per chunk in scalar registers, so that its loads and stores take a fixed per-lane offset and no 64-bit vector
-// address arithmetic.
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc raw_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 
 // ----------------------------------------------------------------------------------------------- phase 1
 

@@ -117,6 +117,18 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int T, int&
   eos = min(max(cu[s + 1], bos), T);
 }
 
+// ------------------------------------------------------------------------------------------ buffer resources
+
+// Buffer resource of a raw byte range (no stride, no swizzle; the 32-bit data format gfx9 takes for untyped
+// accesses): stores at byte offsets past `bytes` are dropped and loads there read zero. Formed in scalar
+// registers, so that loads and stores through it take a per-lane offset and no 64-bit vector address
+// arithmetic, and rows past a range's end need no per-lane condition (a store under a lane condition makes
+// the compiler wait for every outstanding load at the join).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc raw_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // ------------------------------------------------------------------------------------------ chunked prefill
 
 constexpr int CHUNK_LEN = 64;  // tokens per chunk of the chunked (WY / UT form) prefill
