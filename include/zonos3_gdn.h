@@ -311,6 +311,31 @@ int zgdn_accent_shift(const void* x, long x_ld, const void* down, const void* up
                       const void* y_in, long y_in_ld, void* y_out, long y_out_ld, int rows, int in, int out, int K,
                       int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * y = x . w^T on bf16 MFMA with fp32 accumulation, rounded to bf16: the GDN layer's projections, in_proj
+ * (model/src/zonos3/reference/lm.py:561, servers/sgl/src/zonos3_sgl/models/gdn.py:399) and wo (lm.py:602,
+ * gdn.py:447), F.linear without bias.
+ *   x [M, K] (rows x_ld elements apart), w [N, K] (dense, the weight as stored), y [M, N] (rows y_ld apart):
+ *   bf16 (dtype BF16); K a multiple of 128, N, x_ld and y_ld multiples of 8, 16-byte aligned bases.
+ */
+int zgdn_gemm_nt(const void* x, long x_ld, const void* w, void* y, long y_ld, int M, int N, int K, int dtype,
+                 void* stream);
+
+/*
+ * The GDN layer's in_proj with its depthwise causal conv + SiLU fused into the GEMM's epilogue, for one sequence
+ * of M rows: y[:, :C] = silu(conv(x . w[:C]^T)) (the conv output the chunked prefill reads q, k, v from), and
+ * y[:, C:] = x . w[C:]^T (z | a | b, raw). Replaces F.linear + the conv of model/src/zonos3/reference/lm.py:561-568
+ * (and, on the serving path, gdn.py:399 + causal_conv1d_fwd at gdn.py:403-414 for a single request), with
+ * lm.py's rounding points: the projection rounded to bf16, the conv accumulated in fp32 and rounded, the SiLU
+ * rounded again; the projection's raw q|k|v is never written.
+ *   x, w, y, x_ld, y_ld, M, N, K as zgdn_gemm_nt (bf16). C: conv channels (q|k|v), a multiple of 128, <= N.
+ *   conv_weight [C, 4] (tap 0 oldest, 8-byte aligned). hist_in [C, 3]: the raw inputs before row 0, oldest
+ *   first (NULL = zeros); hist_out [C, 3] receives the last 3 raw inputs of [history | rows] (NULL = not
+ *   written; must not be hist_in).
+ */
+int zgdn_in_proj_conv(const void* x, long x_ld, const void* w, void* y, long y_ld, int M, int N, int K,
+                      const void* conv_weight, int C, const void* hist_in, void* hist_out, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,8 @@ def test_header_declares_entry_points():
             "zgdn_accent_shift", "zgdn_chunk_segment_workspace_size", "zgdn_chunk_set_launch_form",
             "zgdn_chunk_get_launch_form", "zgdn_chunk_status", "zgdn_chunk_set_wait_limit",
             "zgdn_chunk_status_async", "zgdn_chunk_overlap_queues",
-            "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc", "zgdn_chunk_workspace_bytes"} == _declared()
+            "zgdn_chunk_noalloc_max_bytes", "zgdn_chunk_fwd_noalloc", "zgdn_chunk_workspace_bytes", "zgdn_gemm_nt",
+            "zgdn_in_proj_conv"} == _declared()
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -108,6 +109,18 @@ def test_bad_arguments_fail_with_a_message(gdn):
     chunk[23] = 1536 + 2
     assert lib.zgdn_chunk_fwd(*chunk) == native.EINVAL and b"multiples of 4" in lib.zgdn_last_error()
     chunk[23], chunk[3] = 128, 1
+    # projection kernels: dtype, K multiple of 128, strides, conv channels, in-place history
+    # (every call here fails validation or has no rows: none launches with these dummy pointers)
+    gemm = [p, 1024, p, p, 2056, 64, 2056, 1000, 1, None]
+    assert lib.zgdn_gemm_nt(*gemm) == native.EINVAL and b"K=1000" in lib.zgdn_last_error()
+    gemm[7], gemm[8] = 1024, 0
+    assert lib.zgdn_gemm_nt(*gemm) == native.EUNSUPPORTED and b"bf16 only" in lib.zgdn_last_error()
+    gemm[8], gemm[5] = 1, 0
+    assert lib.zgdn_gemm_nt(*gemm) == native.OK  # no rows: nothing to launch
+    proj = [p, 1024, p, p, 2056, 64, 2056, 1024, p, 1500, None, None, 1, None]
+    assert lib.zgdn_in_proj_conv(*proj) == native.EINVAL and b"C=1500" in lib.zgdn_last_error()
+    proj[9], proj[10], proj[11] = 1536, p, p
+    assert lib.zgdn_in_proj_conv(*proj) == native.EINVAL and b"in place" in lib.zgdn_last_error()
     # per-dtype workspace: the bf16 path's at 128; 5 fp32 blocks of 64 x D + 256 bytes an item otherwise
     wb = lib.zgdn_chunk_workspace_bytes
     assert wb(64, 16, 128, 128, 1) == lib.zgdn_chunk_workspace_size(64, 16)

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "zgdn_chunk_workspace_size": (c_size_t, [c_int, c_int]),
     "zgdn_chunk_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "zgdn_gemm_nt": (c_int, [_P, c_long, _P, _P, c_long, c_int, c_int, c_int, c_int, _P]),
+    "zgdn_in_proj_conv": (c_int, [_P, c_long, _P, _P, c_long, c_int, c_int, c_int, _P, c_int, _P, _P, c_int, _P]),
     "zgdn_chunk_set_launch_form": (c_int, [c_int]),
     "zgdn_chunk_get_launch_form": (c_int, []),
     "zgdn_chunk_status": (c_int, [POINTER(c_int), c_int]),

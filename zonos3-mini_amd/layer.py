@@ -12,7 +12,9 @@ or ``Zonos3LM._gdn = gdn`` (the class).
 Data path: one row (decode) -> the fused decode-block kernel (conv, SiLU, L2, gate, update, gated norm in
 one launch); more rows -> the conv kernel, then the chunked kernels (bf16 MFMA for bf16 at head size 128, fp32
 arithmetic for fp32 and for 64-wide heads; the recurrent kernel for other head sizes), with the q/k L2-norm and
-the gate formed in the kernel, then the gated-RMSNorm kernel.
+the gate formed in the kernel, then the gated-RMSNorm kernel. A bf16 model without accent adapters (``_lin`` is
+then F.linear, lm.py:505-507) runs its projections on this package's GEMM, in_proj with the conv fused into its
+epilogue.
 """
 
 from __future__ import annotations
@@ -41,14 +43,26 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
     kernel = conv_w.shape[-1]
     n = len(x)
     dev, dt = x.device, x.dtype
-    projection = self._lin(p + "in_proj", x, a.in_proj.weight)
-    qkv, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
+    # the package's projections: a bf16 model whose _lin is plain F.linear (no accent adapters loaded), shapes the
+    # GEMM takes (K a multiple of 128, the conv over whole 128-column tiles)
+    own_proj = (dt == torch.bfloat16 and getattr(self, "_accents", None) is None and kernel == 4 and n > 1
+                and x.shape[-1] % 128 == 0 and inner % 128 == 0 and a.in_proj.weight.dtype == dt
+                and a.wo.weight.dtype == dt)
     history = cache.conv_state.get(layer)  # None before the first call: the kernels read zeros
     state = cache.gdn_state.get(layer)
     A_log, dt_bias = a.A_log.float().contiguous(), a.dt_bias.float().contiguous()
     conv_w = conv_w.to(dt).contiguous()
     norm_w = a.out_weight.to(dt).contiguous()
     capture = getattr(self, "_capture", None) is not None
+
+    if own_proj:
+        h0 = None if history is None else history.reshape(channels, kernel - 1).to(dt).contiguous()
+        projection, new_hist = ops.in_proj_conv(x, a.in_proj.weight, conv_w, channels, initial_state=h0)
+        conv2d = projection[:, :channels]  # silu(conv(q|k|v)): the conv ran in the projection's epilogue
+        _, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
+    else:
+        projection = self._lin(p + "in_proj", x, a.in_proj.weight)
+        qkv, z, aa, b = projection.split((3 * inner, inner, heads, heads), -1)
 
     if n == 1 and hd == 128 and kernel == 4 and not capture:
         # the fused decode block updates conv history and state in place: work on fresh copies
@@ -69,10 +83,12 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
 
     # q|k|v, z, a and b are read in place from the projection rows; the conv output's q, k, v column slices
     # likewise
-    h0 = None if history is None else history.reshape(1, channels, kernel - 1).contiguous()
-    conv, new_hist = ops.causal_conv1d(qkv.unsqueeze(0), conv_w, initial_state=h0, activation="silu",
-                                       state_width=kernel - 1)
-    q, k, v = (part.unflatten(-1, (heads, hd)) for part in conv.split(inner, -1))
+    if not own_proj:
+        h0 = None if history is None else history.reshape(1, channels, kernel - 1).contiguous()
+        conv, new_hist = ops.causal_conv1d(qkv.unsqueeze(0), conv_w, initial_state=h0, activation="silu",
+                                           state_width=kernel - 1)
+        conv2d = conv[0]
+    q, k, v = (part.unflatten(-1, (heads, hd)).unsqueeze(0) for part in conv2d.split(inner, -1))
     s0 = None if state is None else state.reshape(1, heads, hd, hd).float().contiguous()
     kw = dict(initial_state=s0, A_log=A_log, dt_bias=dt_bias, use_qk_l2norm=True)
     if dt in (torch.bfloat16, torch.float32) and hd in (64, 128):
@@ -94,12 +110,14 @@ def gdn(self, x: torch.Tensor, layer: int, cache) -> torch.Tensor:
             beta = ops.sigmoid(b.contiguous(), out_dtype=torch.float32)
         decay = torch.exp(-A_log.exp() * F.softplus(aa.float() + dt_bias))  # diagnostics only
         for name, tensor in (
-            ("gdn_conv", conv[0]), ("gdn_q", qn), ("gdn_k", kn), ("gdn_v", v.reshape(n, heads, hd).float()),
+            ("gdn_conv", conv2d), ("gdn_q", qn), ("gdn_k", kn), ("gdn_v", v.reshape(n, heads, hd).float()),
             ("gdn_decay", decay), ("gdn_beta", beta.reshape(n, heads)), ("gdn_recurrent", recurrent),
             ("gdn_gated", gated), ("gdn_state", cache.gdn_state[layer]),
             ("gdn_conv_state", cache.conv_state[layer]),
         ):
             self._save(f"{name}_{layer}", tensor)
+    if own_proj:
+        return ops.gemm_nt(gated, a.wo.weight)
     return self._lin(p + "wo", gated, a.wo.weight)
 
 

@@ -689,3 +689,60 @@ def accent_shift(x, down, up, mask, y=None, out=None):
                  _ptr(y), y_ld, out.data_ptr(), out_ld, rows, n_in, n_out, K, code, workspace.data_ptr(), ws_bytes,
                  _stream(dev))
     return out
+
+
+def _gemm_operands(name, x, w, dev):
+    x, x_ld = _rows_in_place(name, x, 1, dev, 8, 16)
+    _require(x.dim() == 2, f"{name}: expected [M, K], got {tuple(x.shape)}")
+    _on_gpu("w", w, dev)
+    _require(w.dim() == 2 and w.shape[1] == x.shape[1], f"w: expected [N, {x.shape[1]}], got {tuple(w.shape)}")
+    _require(x.dtype == w.dtype == torch.bfloat16, "the projection kernels take bfloat16 operands")
+    return x, x_ld
+
+
+def gemm_nt(x, w, out=None):
+    """y = x . w^T (F.linear without bias) on bf16 MFMA with fp32 accumulation, rounded to bf16: the GDN layer's
+    projections (in_proj lm.py:561 / gdn.py:399, wo lm.py:602 / gdn.py:447; C ABI ``zgdn_gemm_nt``).
+
+    x [M, K] bfloat16 (rows may be a strided slice), w [N, K] bfloat16 (dense); K a multiple of 128, N of 8.
+    Returns y [M, N] bfloat16 (``out``, when given, is written and returned)."""
+    dev = x.device if isinstance(x, torch.Tensor) else None
+    x, x_ld = _gemm_operands("x", x, w, dev)
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    _require(out.shape == (M, N) and out.dtype == torch.bfloat16 and out.stride(1) == 1,
+             f"out: expected bfloat16 [{M}, {N}] with unit column stride")
+    _native.call("zgdn_gemm_nt", x.data_ptr(), x_ld, w.data_ptr(), out.data_ptr(), out.stride(0), M, N, K, BF16,
+                 _stream(dev))
+    return out
+
+
+def in_proj_conv(x, w, conv_weight, channels, initial_state=None, output_final_state=True):
+    """The GDN layer's in_proj with the depthwise causal conv + SiLU of its q|k|v columns fused in, for one
+    sequence (lm.py:561-568; C ABI ``zgdn_in_proj_conv``): y[:, :C] = silu(conv(x . w[:C]^T)) with the width-4
+    conv over rows (history: the last 3 raw inputs before row 0, oldest first), y[:, C:] = x . w[C:]^T raw.
+
+    x [M, K], w [N, K], conv_weight [C, 4] or [C, 1, 4] bfloat16; ``channels`` = C (a multiple of 128);
+    initial_state [C, 3] bfloat16 or None (zeros). Returns (y [M, N] bfloat16, new history [C, 3] or None)."""
+    dev = x.device if isinstance(x, torch.Tensor) else None
+    x, x_ld = _gemm_operands("x", x, w, dev)
+    M, K = x.shape
+    N, C = w.shape[0], int(channels)
+    if conv_weight.dim() == 3:
+        conv_weight = conv_weight.squeeze(1)
+    _on_gpu("conv_weight", conv_weight, dev)
+    _require(conv_weight.shape == (C, 4) and conv_weight.dtype == torch.bfloat16,
+             f"conv_weight: expected bfloat16 [{C}, 4], got {conv_weight.dtype} {tuple(conv_weight.shape)}")
+    conv_weight = conv_weight.contiguous()
+    if initial_state is not None:
+        _on_gpu("initial_state", initial_state, dev)
+        _require(initial_state.shape == (C, 3) and initial_state.dtype == torch.bfloat16,
+                 f"initial_state: expected bfloat16 [{C}, 3], got {initial_state.dtype} {tuple(initial_state.shape)}")
+        initial_state = initial_state.contiguous()
+    final = torch.empty(C, 3, device=dev, dtype=torch.bfloat16) if output_final_state else None
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    _native.call("zgdn_in_proj_conv", x.data_ptr(), x_ld, w.data_ptr(), y.data_ptr(), N, M, N, K,
+                 conv_weight.data_ptr(), C, _ptr(initial_state), _ptr(final), BF16, _stream(dev))
+    return y, final
