@@ -6,10 +6,12 @@
 //
 // Both operands are K-contiguous, so an MFMA fragment (v_mfma_f32_16x16x32_bf16: lane 16 g + m holds 8
 // consecutive k of row m of A, or of column m of B, i.e. of row m of W) is one 16-byte read of a row. Workgroups
-// of 8 waves own BM x 128 output tiles (BM = 256: waves 4 x 2 of 64 x 64; BM = 128: waves 2 x 4 of 64 x 32) and
-// walk K in blocks of 64 staged through three LDS stages (128-byte rows, 16-byte chunk c of row r at c ^ ((r / 2)
-// % 8), which keeps the 16-row fragment reads free of bank conflicts), filled by direct-to-LDS loads
-// (buffer_load_dwordx4 ... lds): block kb computes while blocks kb + 1 and kb + 2 land. Tiles are grouped so that
+// of 8 waves own BM x 128 output tiles (the launches use BM = 128: waves 2 x 4 of 64 x 32; the configuration also
+// describes BM = 256: waves 4 x 2 of 64 x 64) and
+// walk K in blocks of 64 staged through LDS (128-byte rows, 16-byte chunk c of row r at c ^ ((r / 2) % 8), which
+// keeps the 16-row fragment reads free of bank conflicts), filled by direct-to-LDS loads (buffer_load_dwordx4 ...
+// lds): block kb computes while the next blocks land (three stages for 256-row tiles, one workgroup per CU; two
+// for 128-row tiles, two workgroups per CU). Tiles are grouped so that
 // the workgroups of one XCD (workgroups go round-robin over the 8 XCDs) share a 4 x 8 block of tiles and read
 // their operands once into that XCD's L2. Columns past the last multiple of 128 (in_proj's a | b: 2056 = 16 x 128
 // + 8) are taken by a strip kernel.
@@ -36,7 +38,6 @@ typedef float gf32x4 __attribute__((ext_vector_type(4)));
 constexpr int GK = 64;         // K block (two MFMA k-steps)
 constexpr int GBN = 128;       // tile columns
 constexpr int GTHREADS = 512;  // 8 waves
-constexpr int GSTAGES = 3;     // LDS stages
 constexpr int HALO = 16;       // rows above a conv tile computed again
 constexpr int CW = 4;          // conv width (the model's GDN_KERNEL)
 
@@ -65,7 +66,11 @@ struct GemmCfg {
     static constexpr int BYTES = PIECES * 1024;
     static constexpr int MAXP = (PIECES + 7) / 8;  // pieces per wave (at most)
   };
-  static constexpr int LDS = GSTAGES * St<true, true>::BYTES;
+  // LDS stages: three for 256-row tiles (one workgroup per CU), two for 128-row tiles (two workgroups per CU,
+  // so that one's epilogue runs beside the other's MFMAs)
+  static constexpr int STAGES = BM == 256 ? 3 : 2;
+  static constexpr int WG_PER_CU = BM == 256 ? 1 : 2;
+  static constexpr int LDS = STAGES * St<true, true>::BYTES;
 };
 
 // A stage's pieces: piece p (1 KiB of LDS at stage + 1024 p) goes to wave p % 8; pieces below A_PIECES hold rows
@@ -163,18 +168,22 @@ __device__ __forceinline__ void k_loop(const uint16_t* X, long x_ld, const uint1
   const int nk = K / GK;
   const int mine = (S::PIECES - wave + 7) / 8;  // this wave's pieces per block
   const int l = threadIdx.x & 63, m = l & 15, g = l >> 4;
-  gload_lds<BM, H, R>(src, lds, 0, wave);
-  gload_lds<BM, H, R>(src, lds + S::BYTES, min(1, nk - 1), wave);
-  // Block kb computes from stage kb % 3. A wave waits for its own loads of block kb (those of block kb + 1 may
-  // stay outstanding), the barrier for everyone's and for every wave to be done with the stage the next loads
-  // overwrite. Past the last block the last one is loaded again (into a stage nothing reads), so that the wait
-  // count stays the same.
+  constexpr int NS = C::STAGES;
+#pragma unroll
+  for (int q = 0; q < NS - 1; ++q) gload_lds<BM, H, R>(src, lds + q * S::BYTES, min(q, nk - 1), wave);
+  // Block kb computes from stage kb % NS. A wave waits for its own loads of block kb (those of the blocks after
+  // it may stay outstanding), the barrier for everyone's and for every wave to be done with the stage the next
+  // loads overwrite. Past the last block the last one is loaded again (into a stage nothing reads), so that the
+  // wait count stays the same.
   int st = 0;
   for (int kb = 0; kb < nk; ++kb) {
-    wait_pieces(mine);
+    if constexpr (NS == 3)
+      wait_pieces(mine);
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    const int stn = st == 0 ? GSTAGES - 1 : st - 1;  // stage of block kb + 2 (= that of block kb - 1)
-    gload_lds<BM, H, R>(src, lds + stn * S::BYTES, min(kb + 2, nk - 1), wave);
+    const int stn = st == 0 ? NS - 1 : st - 1;  // stage of block kb + NS - 1 (= that of block kb - 1)
+    gload_lds<BM, H, R>(src, lds + stn * S::BYTES, min(kb + NS - 1, nk - 1), wave);
     const uint8_t* a_st = lds + st * S::BYTES;
     const uint8_t* b_st = a_st + S::A_PIECES * 1024;
 #pragma unroll
@@ -206,7 +215,7 @@ __device__ __forceinline__ void k_loop(const uint16_t* X, long x_ld, const uint1
         }
       }
     }
-    st = st == GSTAGES - 1 ? 0 : st + 1;
+    st = st == NS - 1 ? 0 : st + 1;
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -232,7 +241,7 @@ __device__ __forceinline__ void stage_out(uint16_t* out, int row0, const Acc<BM>
 // (X and W are not __restrict__: as restrict-qualified read-only data their loads could be moved past the LDS
 // barriers.)
 template <int BM, bool CONV, bool R>
-__global__ __launch_bounds__(GTHREADS, 1) void gemm_kernel(const uint16_t* X, long x_ld, const uint16_t* W,
+__global__ __launch_bounds__(GTHREADS, GemmCfg<BM>::WG_PER_CU) void gemm_kernel(const uint16_t* X, long x_ld, const uint16_t* W,
                                                            uint16_t* __restrict__ Y, long y_ld, int M, int N, int K,
                                                            int tiles_m, int tiles_n, const uint16_t* __restrict__ conv_w,
                                                            int C, const uint16_t* __restrict__ hist_in,
@@ -331,6 +340,7 @@ __global__ __launch_bounds__(GTHREADS, 1) void gemm_kernel(const uint16_t* X, lo
     }
     auto px = [&](int r) { return *reinterpret_cast<const uint32_t*>(out + (HALO + r) * GBN + 2 * cp); };
     uint32_t h0 = px(r0 - 3), h1 = px(r0 - 2), h2 = px(r0 - 1);
+#pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
       const int r = r0 + rr;
       const uint32_t xv = px(r);
@@ -422,27 +432,16 @@ bool gemm_lds_ready() {
   return ok;
 }
 
-int gemm_cus() {
-  static std::atomic<int> cached{0};
-  int n = cached.load(std::memory_order_relaxed);
-  if (n > 0) return n;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n < 1)
-    n = 256;
-  cached.store(n, std::memory_order_relaxed);
-  return n;
-}
-
 template <bool CONV>
 int gemm_launch(const char* fn, const void* x, long x_ld, const void* w, void* y, long y_ld, int M, int N, int K,
                 const void* conv_w, int C, const void* hist_in, void* hist_out, hipStream_t s) {
   const int n_full_cols = N / GBN, n_rem0 = n_full_cols * GBN;
   bool strip = n_rem0 < N;
   if (n_full_cols > 0) {
-    // 256-row tiles when they fill the device once, else 128-row ones; a remainder of at most 16 columns formed
-    // by the tiles when their column count covers a row block in 16-row pieces
-    const bool big = (long)((M + 255) / 256) * n_full_cols >= gemm_cus();
+    // 128-row tiles, two workgroups a CU: measured faster than 256-row tiles at one a CU for every shape of the
+    // layer (in_proj 4096 x 2056 x 1024: 22.3 against 24.7 us; 4096 x 2048 x 1024: 21.1 against 24.1 us), as one
+    // workgroup's epilogue (the conv's VALU work) runs beside the other's MFMAs. A remainder of at most 16
+    // columns is formed by the tiles when their column count covers a row block in 16-row pieces.
 #define ZGDN_GEMM(BMV, RV)                                                                                          \
   do {                                                                                                              \
     if (!gemm_lds_ready<BMV, CONV, RV>()) return fail(ZGDN_EHIP, "%s: the device refused the GEMM's LDS", fn);     \
@@ -451,15 +450,11 @@ int gemm_launch(const char* fn, const void* x, long x_ld, const void* w, void* y
                        (const uint16_t*)x, x_ld, (const uint16_t*)w, (uint16_t*)y, y_ld, M, N, K, tm, n_full_cols, \
                        (const uint16_t*)conv_w, C, (const uint16_t*)hist_in, (uint16_t*)hist_out);                 \
   } while (0)
-    const int bm = big ? 256 : 128;
-    const bool fold = strip && N - n_rem0 <= 16 && 16 * n_full_cols >= bm;
-    if (big) {
-      if (fold) ZGDN_GEMM(256, true);
-      else ZGDN_GEMM(256, false);
-    } else {
-      if (fold) ZGDN_GEMM(128, true);
-      else ZGDN_GEMM(128, false);
-    }
+    const bool fold = strip && N - n_rem0 <= 16 && 16 * n_full_cols >= 128;
+    if (fold)
+      ZGDN_GEMM(128, true);
+    else
+      ZGDN_GEMM(128, false);
 #undef ZGDN_GEMM
     strip = strip && !fold;
   }
