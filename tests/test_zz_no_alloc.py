@@ -2,7 +2,10 @@
 per-device static scratch), called through the C ABI with caller-allocated outputs: on two calls in a row, the
 second smaller, its outputs and final states equal zgdn_chunk_fwd's on the same inputs bit for bit (the same
 kernels; the scratch keeps the first call's contents, so anything the second call read without writing would
-show) and sit within tolerance of the oracle (bf16: outputs 2e-2 max-abs, states 1e-3 relative). A call whose
+show) and sit within tolerance of the oracle (bf16: outputs 2e-2 max-abs, states 1e-3 relative). The same holds
+for each of the path's launch forms in the scratch: the plain two launches, the overlapped launch (whose control
+block in the scratch must start each call at zero) and the segmented state pass (whose extra space follows the
+workspace in the scratch); and for calls captured into a HIP graph and replayed with new inputs. A call whose
 workspace exceeds the scratch is refused before any launch."""
 
 from __future__ import annotations
@@ -88,3 +91,67 @@ def test_noalloc_refuses_more_than_its_scratch(gdn, cuda):
                                     128**-0.5, None)
     assert st == gdn._native.EINVAL
     assert b"scratch" in lib.zgdn_last_error()
+
+
+def _pair(gdn, cuda, B, T, H, seed):
+    """One no-alloc call and one zgdn_chunk_fwd call on the same inputs (zero initial states); both results."""
+    d, x = _case(cuda, B, T, H, H, seed=seed)
+    o = torch.empty(B, T, H, 128, dtype=torch.bfloat16, device=cuda)
+    final = torch.empty(B, H, 128, 128, device=cuda)
+    _noalloc(gdn, x, o, final, None)
+    o_ref, s_ref = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
+    torch.cuda.synchronize()
+    return d, o, final, o_ref, s_ref
+
+
+def test_noalloc_overlapped_launch_on_two_calls(gdn, cuda):
+    """The overlapped launch (forced) in the scratch: its control block (tickets, per-CU claims, ready flags)
+    lies in the scratch after the workspace and must be zeroed by each call; a second, smaller call reuses it."""
+    with gdn.ops.launch_form(1):
+        for B, T, H, seed in [(1, 4096, 8, 7101), (1, 2048, 8, 7102)]:
+            announce(f"chunk no-alloc overlapped B={B} T={T} H={H}")
+            d, o, final, o_ref, s_ref = _pair(gdn, cuda, B, T, H, seed)
+            assert torch.equal(o, o_ref) and torch.equal(final, s_ref)
+            o_cpu, s_cpu = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+            assert max_abs(o.cpu(), o_cpu) < 2e-2 and rel_err(final.cpu(), s_cpu) < 1e-3
+    assert gdn.ops.chunk_status() == 0
+
+
+def test_noalloc_segmented_pass_on_two_calls(gdn, cuda):
+    """Few long chains (one 4096- then 3072-token prompt, 4 heads) take the segmented state pass, whose local
+    and transition states, Q'P^T rows and segment starts sit in the scratch after the phase-1 workspace."""
+    lib = gdn._native.lib()
+    for B, T, H, seed in [(1, 4096, 4, 7201), (1, 3072, 4, 7202)]:
+        assert lib.zgdn_chunk_segment_workspace_size(B, T, H) > 0  # the library plans segments here
+        announce(f"chunk no-alloc segmented B={B} T={T} H={H}")
+        d, o, final, o_ref, s_ref = _pair(gdn, cuda, B, T, H, seed)
+        assert torch.equal(o, o_ref) and torch.equal(final, s_ref)
+        o_cpu, s_cpu = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"])
+        assert max_abs(o.cpu(), o_cpu) < 2e-2 and rel_err(final.cpu(), s_cpu) < 1e-3
+
+
+@pytest.mark.parametrize("form", [0, 1])
+def test_noalloc_in_a_graph(gdn, cuda, form):
+    """A no-alloc call captured into a HIP graph (two launches, or the overlapped launch with its control-block
+    fill kernel) and replayed three times, with new inputs copied in and eager work in between: every replay
+    equals zgdn_chunk_fwd on the same inputs bit for bit."""
+    announce(f"chunk no-alloc graph form={form}")
+    B, T, H = 1, 1024, 8
+    _, x = _case(cuda, B, T, H, H, seed=7300)
+    o = torch.empty(B, T, H, 128, dtype=torch.bfloat16, device=cuda)
+    final = torch.empty(B, H, 128, 128, device=cuda)
+    with gdn.ops.launch_form(form):
+        _noalloc(gdn, x, o, final, x["s0"])  # first call on the device outside the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            _noalloc(gdn, x, o, final, x["s0"])
+        for r in range(3):
+            _, new = _case(cuda, B, T, H, H, seed=7301 + r)
+            for name in ("q", "k", "v", "g", "beta", "s0"):
+                x[name].copy_(new[name])
+            graph.replay()
+            o_ref, s_ref = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"])
+            torch.cuda.synchronize()
+            assert torch.equal(o, o_ref) and torch.equal(final, s_ref), r
+    assert gdn.ops.chunk_status() == 0
