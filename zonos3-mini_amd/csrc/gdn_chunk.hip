@@ -165,7 +165,7 @@ constexpr int PS_K = 32768;        // k rows [64][128] bf16
 constexpr int PS_V = 49152;        // v rows
 constexpr int PS_PT = 65536;       // P^T bf16 [64][64]; the blocks of zeros above P's diagonal blocks set once
 constexpr int PS_F = 73728;        // per-token factors: 8 x 64 floats
-constexpr int PSF_G = 0, PSF_B = 256, PSF_RK = 512, PSF_AI = 768, PSF_PI = 1024, PSF_BK = 1280, PSF_FQ = 1536,
+constexpr int PSF_G = 0, PSF_B = 256, PSF_H = 512, PSF_UA = 768, PSF_UP = 1024, PSF_BK = 1280, PSF_FQ = 1536,
               PSF_FK = 1792;
 constexpr int PS_BYTES = PS_F + 2048;  // 75,776
 struct alignas(16) PrepShared {
@@ -278,14 +278,77 @@ struct RowRegs {
   uint4 q0, q1, k0, k1, v0, v1;
 };
 
+// Where a phase-1 item's rows lie: chunk c (its token range cr), value head h and key head hk.
+struct ItemAt {
+  int c, h, hk;
+  ChunkRange cr;
+};
+__device__ __forceinline__ ItemAt item_at(int item, const int32_t* cu, const int32_t* chunk_idx, int n_seqs, int T,
+                                          int Hk, int Hv) {
+  ItemAt a;
+  a.c = item / Hv;
+  a.h = item % Hv;
+  a.hk = a.h / (Hv / Hk);
+  a.cr = chunk_range(a.c, cu, chunk_idx, T, n_seqs);
+  return a;
+}
+
+// The items item0, item0 + stride, ... of a persistent workgroup with their positions carried from one to the
+// next by additions (item = c Hv + h, and for B x T batches c = b nt + j with nt chunks a row): the integer
+// divisions of item_at, each a dozen vector instructions (no scalar divide), are taken once per workgroup.
+struct ItemWalk {
+  int item, c, h, b, j;
+  int stride, dc, dh, db, dj, Hv, nt, grp;
+  uint32_t mg;  // ceil(2^32 / grp): h / grp = umulhi(h, mg), exact for h, grp < 2^16
+  __device__ __forceinline__ ItemWalk(int item0, int stride_, int Hv_, int Hk, int T)
+      : item(item0), stride(stride_), Hv(Hv_) {
+    c = item0 / Hv;
+    h = item0 % Hv;
+    dc = stride / Hv;
+    dh = stride % Hv;
+    nt = max(1, (T + CH - 1) / CH);
+    b = c / nt;
+    j = c % nt;
+    db = dc / nt;
+    dj = dc % nt;
+    grp = Hv / Hk;
+    mg = grp > 1 ? 0xffffffffu / (uint32_t)grp + 1u : 0u;
+  }
+  __device__ __forceinline__ void advance() {
+    item += stride;
+    h += dh;
+    const int carry = h >= Hv ? 1 : 0;
+    h -= carry * Hv;
+    c += dc + carry;
+    j += dj + carry;
+    b += db;
+    if (j >= nt) {
+      j -= nt;
+      ++b;
+    }
+  }
+  __device__ __forceinline__ ItemAt at(const int32_t* cu, const int32_t* chunk_idx, int n_seqs, int T) const {
+    ItemAt a;
+    a.c = c;
+    a.h = h;
+    a.hk = grp > 1 ? (int)__umulhi((uint32_t)h, mg) : h;
+    if (cu != nullptr) {
+      a.cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+    } else {
+      a.cr.t0 = b * T + j * CH;
+      a.cr.len = min(CH, T - j * CH);
+    }
+    return a;
+  }
+};
+
 // The chunk's rows of q, k, v for thread (rr, c8): rows rr and rr + 32, columns c8 .. c8 + 7 (zeros past the
 // chunk end).
-__device__ __forceinline__ void load_rows(RowRegs& R, int item, const uint16_t* q, const uint16_t* k,
-                                          const uint16_t* v, const int32_t* cu, const int32_t* chunk_idx, int n_seqs,
-                                          int T, int Hk, int Hv, const RowStrides& rs, uint32_t oq, uint32_t ok,
+__device__ __forceinline__ void load_rows(RowRegs& R, const ItemAt& it, const uint16_t* q, const uint16_t* k,
+                                          const uint16_t* v, const RowStrides& rs, uint32_t oq, uint32_t ok,
                                           uint32_t ov) {
-  const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
-  const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+  const ChunkRange cr = it.cr;
+  const int h = it.h, hk = it.hk;
   const Rsrc rq = rows_rsrc(q, cr.t0, rs.q, hk * DK, cr.len), rk = rows_rsrc(k, cr.t0, rs.k, hk * DK, cr.len);
   const Rsrc rv = rows_rsrc(v, cr.t0, rs.v, h * DV, cr.len);
   R.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq, 0, 0));
@@ -312,14 +375,13 @@ __device__ __forceinline__ void prep_init(uint8_t* lb) {
 // workspace is read back by the item).
 __device__ __forceinline__ void item_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// One phase-1 item. `R` holds the item's rows (loaded by the caller); `next` (>= 0) is the item whose rows
-// are loaded into R while this one computes. Ends with a workgroup barrier.
+// One phase-1 item (`it`). `R` holds the item's rows (loaded by the caller); with `has_next`, the rows of item
+// `nx` are loaded into R while this one computes. Ends with a workgroup barrier.
 template <typename TG, bool GATE>
-__device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int next,
+__device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs& R, bool has_next, const ItemAt& nx,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
-    const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
-    int n_seqs, int T, int Hk, int Hv, float scale, int qk_l2norm, const RowStrides& rs,
+    const float* __restrict__ dt_bias, int Hv, float scale, int qk_l2norm, const RowStrides& rs,
     uint8_t* __restrict__ ws, const PrepLane& L0, int rowoff, uint32_t oq, uint32_t ok, uint32_t ov) {
   // the lane offsets pass through an empty asm per item: the compiler then forms the addresses derived from
   // them inside the item (most fold into instruction offsets) instead of hoisting every one of them out of the
@@ -333,8 +395,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int
   asm volatile("" : "+v"(tid));
   const int l = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = l & 15, gq = l >> 4;
-  const int c = item / Hv, h = item % Hv, hk = h / (Hv / Hk);
-  const ChunkRange cr = chunk_range(c, cu, chunk_idx, T, n_seqs);
+  const int c = it.c, h = it.h, hk = it.hk;
+  const ChunkRange cr = it.cr;
   uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
   float* F = reinterpret_cast<float*>(lb + PS_F);
 
@@ -356,7 +418,7 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int
   lds_put<uint4>(lb, PS_K + rowoff + 8192, R.k1);
   lds_put<uint4>(lb, PS_V + rowoff, R.v0);
   lds_put<uint4>(lb, PS_V + rowoff + 8192, R.v1);
-  if (next >= 0) load_rows(R, next, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, oq, ok, ov);
+  if (has_next) load_rows(R, nx, q, k, v, rs, oq, ok, ov);
   if (wave == P1_WAVES - 1) {
     if (l < cr.len) {
       if constexpr (GATE) gi = -__expf(alog) * softplus(gi + dtb);
@@ -394,14 +456,14 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int
       }
       rf = rsqrtf(ss + 1e-6f);
     }
-    const float gr = F[(PSF_G >> 2) + r];
+    const float gr = F[(PSF_G >> 2) + r], g2 = gr * 1.44269504088896341f;  // G in log2 units
     if (tid < CH) {
-      F[(PSF_PI >> 2) + r] = scale * rf;
+      F[(PSF_UP >> 2) + r] = g2 + __builtin_amdgcn_logf(scale * rf);
       F[(PSF_FQ >> 2) + r] = scale * __expf(gr) * rf;
     } else {
       const float br = F[(PSF_B >> 2) + r];
-      F[(PSF_RK >> 2) + r] = rf;
-      F[(PSF_AI >> 2) + r] = br * rf;
+      F[(PSF_H >> 2) + r] = g2 - __builtin_amdgcn_logf(rf);
+      F[(PSF_UA >> 2) + r] = g2 + __builtin_amdgcn_logf(br * rf);  // (-inf for beta = 0: those rows of A are 0)
       F[(PSF_FK >> 2) + r] = __expf(F[(PSF_G >> 2) + CH - 1] - gr) * rf;
       F[(PSF_BK >> 2) + r] = br * __expf(gr) * rf;
     }
@@ -447,17 +509,19 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, int item, RowRegs& R, int
   item_barrier();  // A^T overwrites the q rows; the factors are visible
 
   // 3. scaled tiles -> A^T (fp32) and P^T (bf16); wave 0: the diagonal blocks, then their inverse
-  // A_ij = beta_i rk_i exp(G_i - G_j) rk_j k_i.k_j (i > j), P_ij = s rq_i exp(G_i - G_j) rk_j q_i.k_j (i >= j)
+  // A_ij = beta_i rk_i exp(G_i - G_j) rk_j k_i.k_j (i > j), P_ij = s rq_i exp(G_i - G_j) rk_j q_i.k_j (i >= j),
+  // each factor as one exp2(u_i - h_j): u_i = log2(beta_i rk_i) + G_i log2(e) (A) or log2(s rq_i) +
+  // G_i log2(e) (P), h_j = G_j log2(e) - log2(rk_j); only the diagonal tiles need the triangle mask
   auto scale_tile = [&](f32x4 a, int rb, int cb, bool qk) {
     const int j = 16 * cb + m, i0 = 16 * rb + 4 * gq;
-    const float gj = F[(PSF_G >> 2) + j], rkj = F[(PSF_RK >> 2) + j];
-    const f32x4 gi4 = lds_at<f32x4>(lb, PS_F + PSF_G + 4 * i0);
-    const f32x4 fi4 = lds_at<f32x4>(lb, PS_F + (qk ? PSF_PI : PSF_AI) + 4 * i0);
+    const float hj = F[(PSF_H >> 2) + j];
+    const f32x4 u4 = lds_at<f32x4>(lb, PS_F + (qk ? PSF_UP : PSF_UA) + 4 * i0);
     f32x4 e;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = fi4[r] * __expf(gi4[r] - gj) * rkj * a[r];
-      e[r] = (qk ? i0 + r >= j : i0 + r > j) ? x : 0.f;
+    for (int r = 0; r < 4; ++r) e[r] = a[r] * __builtin_amdgcn_exp2f(u4[r] - hj);
+    if (rb == cb) {  // (wave-uniform)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e[r] = (qk ? i0 + r >= j : i0 + r > j) ? e[r] : 0.f;
     }
     return e;
   };
@@ -708,12 +772,18 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
   const PrepRows lr(threadIdx.x, rs);
   prep_init(lb);
   RowRegs R;
-  int item = blockIdx.x;
-  if (item < n_items) load_rows(R, item, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
-  for (; item < n_items; item += gridDim.x) {
-    const int next = item + (int)gridDim.x < n_items ? item + (int)gridDim.x : -1;
-    prep_item<TG, GATE>(lb, item, R, next, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, T, Hk, Hv,
-                        scale, qk_l2norm, rs, ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
+  ItemWalk w(blockIdx.x, gridDim.x, Hv, Hk, T);
+  if (w.item >= n_items) return;
+  ItemAt cur = w.at(cu, chunk_idx, n_seqs, T);  // (a packed batch's chunk table is read for items < n_items only)
+  load_rows(R, cur, q, k, v, rs, lr.oq, lr.ok, lr.ov);
+  while (w.item < n_items) {
+    w.advance();
+    const bool has_next = w.item < n_items;
+    ItemAt nx = cur;
+    if (has_next) nx = w.at(cu, chunk_idx, n_seqs, T);
+    prep_item<TG, GATE>(lb, cur, R, has_next, nx, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs, ws, L,
+                        lr.rowoff, lr.oq, lr.ok, lr.ov);
+    cur = nx;
   }
 }
 
@@ -1300,20 +1370,23 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
   __syncthreads();
   int cur = tk;
   __syncthreads();  // every thread has read tk
-  if (cur >= 0 && cur < n_items) load_rows(R, cur, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
+  if (cur >= 0 && cur < n_items)
+    load_rows(R, item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
   while (cur >= 0) {
     if (threadIdx.x == 0) tk = take();
     __syncthreads();  // tk visible (and the LDS of the last item is free)
     const int nxt = tk;
     const int nload = nxt >= 0 && nxt < n_items ? nxt : -1;
     if (cur < n_items) {
-      prep_item<TG, GATE>(sm.p.b, cur, R, nload, q, k, v, g, beta, A_log, dt_bias, cu, chunk_idx, n_seqs, T, Hk, Hv,
-                          scale, qk_l2norm, rs, ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
+      const ItemAt ic = item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
+      const ItemAt in = item_at(nload >= 0 ? nload : cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
+      prep_item<TG, GATE>(sm.p.b, ic, R, nload >= 0, in, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs,
+                          ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
       __syncthreads();
       if (threadIdx.x == 0) __hip_atomic_store(ctl.flags + cur, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
-      if (nload >= 0) load_rows(R, nload, q, k, v, cu, chunk_idx, n_seqs, T, Hk, Hv, rs, lr.oq, lr.ok, lr.ov);
+      if (nload >= 0) load_rows(R, item_at(nload, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
       __syncthreads();  // every thread has read tk
     }
     cur = nxt;
