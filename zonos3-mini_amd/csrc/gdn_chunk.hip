@@ -376,8 +376,10 @@ __device__ __forceinline__ void prep_init(uint8_t* lb) {
 __device__ __forceinline__ void item_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // One phase-1 item (`it`). `R` holds the item's rows (loaded by the caller); with `has_next`, the rows of item
-// `nx` are loaded into R while this one computes. Ends with a workgroup barrier.
-template <typename TG, bool GATE>
+// `nx` are loaded into R while this one computes. QL: the raw q of the Q' step is taken from the q rows in LDS
+// (held in registers from step 2 on; no second read of q from memory), else read again from memory before step
+// 6 (fewer registers held: the overlapped kernel's budget). Ends with a workgroup barrier.
+template <typename TG, bool GATE, bool QL>
 __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs& R, bool has_next, const ItemAt& nx,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
@@ -466,6 +468,19 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
       F[(PSF_UA >> 2) + r] = g2 + __builtin_amdgcn_logf(br * rf);  // (-inf for beta = 0: those rows of A are 0)
       F[(PSF_FK >> 2) + r] = __expf(F[(PSF_G >> 2) + CH - 1] - gr) * rf;
       F[(PSF_BK >> 2) + r] = br * __expf(gr) * rf;
+    }
+  }
+  // raw q of this wave's Q' jobs (step 8): token 16 tb + m, columns 32 kq + 4 gq .. + 3 and 16 further; with QL
+  // from the q rows, before A^T overwrites them (rows past the chunk end hold zeros)
+  uint2 cq[2][2];
+  if constexpr (QL) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
+      const int tok = 16 * tb + m, cc = 4 * kq + (gq >> 1);
+      const int at = PS_Q + tok * 256 + 8 * (gq & 1);
+      cq[n][0] = lds_at<uint2>(lb, at + ((cc ^ m) << 4));
+      cq[n][1] = lds_at<uint2>(lb, at + (((cc + 2) ^ m) << 4));
     }
   }
   f32x4 acc[4];
@@ -621,17 +636,17 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   }
   item_barrier();
 
-  // raw q of this wave's Q' jobs (step 8), loaded now so the latency is covered
-  uint2 cq[2][2];
+  if constexpr (!QL) {
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
-    const int tok = 16 * tb + m;
-    cq[n][0] = cq[n][1] = make_uint2(0, 0);
-    if (tok < cr.len) {
-      const uint16_t* qrow = q + (size_t)(cr.t0 + tok) * rs.q + hk * DK + 32 * kq + 4 * gq;
-      cq[n][0] = *reinterpret_cast<const uint2*>(qrow);
-      cq[n][1] = *reinterpret_cast<const uint2*>(qrow + 16);
+    for (int n = 0; n < 2; ++n) {
+      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
+      const int tok = 16 * tb + m;
+      cq[n][0] = cq[n][1] = make_uint2(0, 0);
+      if (tok < cr.len) {
+        const uint16_t* qrow = q + (size_t)(cr.t0 + tok) * rs.q + hk * DK + 32 * kq + 4 * gq;
+        cq[n][0] = *reinterpret_cast<const uint2*>(qrow);
+        cq[n][1] = *reinterpret_cast<const uint2*>(qrow + 16);
+      }
     }
   }
 
@@ -781,7 +796,7 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
     const bool has_next = w.item < n_items;
     ItemAt nx = cur;
     if (has_next) nx = w.at(cu, chunk_idx, n_seqs, T);
-    prep_item<TG, GATE>(lb, cur, R, has_next, nx, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs, ws, L,
+    prep_item<TG, GATE, true>(lb, cur, R, has_next, nx, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs, ws, L,
                         lr.rowoff, lr.oq, lr.ok, lr.ov);
     cur = nx;
   }
@@ -1380,7 +1395,7 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
     if (cur < n_items) {
       const ItemAt ic = item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
       const ItemAt in = item_at(nload >= 0 ? nload : cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
-      prep_item<TG, GATE>(sm.p.b, ic, R, nload >= 0, in, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs,
+      prep_item<TG, GATE, false>(sm.p.b, ic, R, nload >= 0, in, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs,
                           ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
       __syncthreads();
