@@ -810,11 +810,12 @@ constexpr int P2_WAVES = 8;
 // (the prefetch of the next chunk stays in flight across it).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Operands of one chunk held in registers (prefetched one chunk ahead).
+// Operands of one chunk held in registers (prefetched one chunk ahead), for a workgroup of NV value blocks.
+template <int NV>
 struct Pre {
   bf16x8 A[4];   // W' (U role) or Q' (O role) fragments of this wave's 16 tokens, k-steps 0..3
   bf16x8 KT[2];  // K^T fragments of this wave's 16 state columns, token steps 0, 1
-  uint4 X;       // U role: Ub' (4 fp32); O role: Ob (4 bf16 in .x, .y)
+  uint4 X[NV];   // per value block, U role: Ub' (4 fp32); O role: Ob (4 bf16 in .x, .y)
   float GL;      // G at the chunk end
 };
 
@@ -822,11 +823,13 @@ struct Pre {
 // The state slice sits in 256-byte rows with 16-byte chunk c of row r at chunk c ^ r (r < 16): its fragment
 // reads (16 rows at one chunk) then meet every bank once. (With padded 272-byte rows each of those reads took
 // 8 LDS cycles, 4 of them bank conflicts, against 4 and none: measured with the hardware counters.)
-struct StateShared {
-  uint16_t Ss[VB * DK];   // state slice (bf16), key columns at positions pi(key): B operand of [W'; Q'] S^T
-  uint16_t UhT[VB][LDC];  // U'^T, hi part   } A operands of the state update
-  uint16_t UlT[VB][LDC];  // U'^T, lo part   }
+template <int NV>
+struct StateSharedT {
+  uint16_t Ss[NV * VB * DK];   // state slice (bf16), key columns at positions pi(key): B operand of [W'; Q'] S^T
+  uint16_t UhT[NV * VB][LDC];  // U'^T, hi part   } A operands of the state update
+  uint16_t UlT[NV * VB][LDC];  // U'^T, lo part   }
 };
+using StateShared = StateSharedT<1>;
 __device__ __forceinline__ int ss_at(int r, int c) { return r * DK + ((((c >> 3) ^ r) & 15) << 3) + (c & 7); }
 
 struct StateArgs {
@@ -861,14 +864,15 @@ __device__ __forceinline__ int load_flag(const int* f) {
 // this job's columns up to the chunk's last token, so rows past the end of a partial chunk are dropped by the
 // range check instead of a per-row condition.
 template <typename TOut>
-__device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci, int t0, int j, const float* ov) {
+__device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int vb, int ci, int t0, int j,
+                                             const float* ov) {
   const bool odd = (lane_id() & 1) != 0;
   const float r0 = dpp<DPP_QUAD_XOR1>(odd ? ov[0] : ov[2]), r1 = dpp<DPP_QUAD_XOR1>(odd ? ov[1] : ov[3]);
   // even lane (column j): rows t0, t0+1 as (own, partner); odd lane (column j): rows t0+2, t0+3 as (partner, own)
   const float a0 = odd ? r0 : ov[0], b0 = odd ? ov[2] : r0, a1 = odd ? r1 : ov[1], b1 = odd ? ov[3] : r1;
   const int tr = t0 + (odd ? 2 : 0), tlen = min(CH, a.len - ci * CH);
   const uint32_t row = (uint32_t)a.Hv * DV * (uint32_t)sizeof(TOut);  // bytes from one token to the next
-  const Rsrc r = raw_rsrc(o + ((size_t)(a.bos + ci * CH) * a.Hv + a.h) * DV + a.vb * VB, (uint32_t)tlen * row);
+  const Rsrc r = raw_rsrc(o + ((size_t)(a.bos + ci * CH) * a.Hv + a.h) * DV + vb * VB, (uint32_t)tlen * row);
   const uint32_t off = (uint32_t)tr * row + (uint32_t)(j & ~1) * (uint32_t)sizeof(TOut);
   if constexpr (sizeof(TOut) == 2) {
     __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(a0, b0), r, off, 0, 0);
@@ -882,9 +886,10 @@ __device__ __forceinline__ void store_o_tile(TOut* o, const StateArgs& a, int ci
 
 // The chunk loop of one wave. URole: waves 0-3 form U' = Ub' - W' S^T of their 16 tokens; the O role
 // (waves 4-7) forms the outputs O = Ob + Q' S^T of their 16 tokens. Both run the same barriers and each
-// wave updates 16 columns of the state slice.
-template <bool URole, typename TOut, bool Wait>
-__device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, TOut* o, f32x4& S) {
+// wave updates 16 columns of the state slice. The slice holds NV blocks of 16 value rows (a.vb .. a.vb + NV -
+// 1): every operand fetched for a chunk but Ub' / Ob serves all of them.
+template <bool URole, typename TOut, bool Wait, int NV>
+__device__ __forceinline__ void state_loop(StateSharedT<NV>& sh, const StateArgs& a, TOut* o, f32x4 (&S)[NV]) {
   const int l = lane_id(), wave = threadIdx.x >> 6;
   const int tb = wave & 3;               // this wave's token tile
   const int j = l & 15;                  // value row within the slice (D layout column of [W'; Q'] S^T)
@@ -895,6 +900,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   // pcol) and its fragments (row l%16, columns 32 kk + 8 (l/16) ..)
   // (the fragment addresses in 16-byte chunks, so that the compiler sees their alignment and keeps each read
   // one 16-byte access)
+  // (block v of the slice at rows 16 v ..: + 16 v DK elements, 2 v DK 16-byte chunks)
   int ss_w[4], ss_r[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -909,27 +915,31 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   const uint32_t offA = (uint32_t)(URole ? WS_WP : WS_QP) + (uint32_t)(tb * 4 * 64 + l) * 16u;
   const uint32_t offX = URole ? (uint32_t)WS_UB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 16u
                               : (uint32_t)WS_OB + (uint32_t)((a.vb * 4 + tb) * 64 + l) * 8u;
+  constexpr uint32_t XB = URole ? 4u * 64u * 16u : 4u * 64u * 8u;  // from one value block's Ub' / Ob to the next
   const uint32_t offK = (uint32_t)WS_KT + (uint32_t)(wave * 2 * 64 + l) * 16u;
   auto ld16 = [](Rsrc w, uint32_t off) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(w, off, 0, 0));
   };
   // the next chunk's loads in groups spread over the phases of the current chunk
-  auto fetch1 = [&](Rsrc w, Pre& x) {
+  auto fetch1 = [&](Rsrc w, Pre<NV>& x) {
     x.A[0] = ld16(w, offA);
     x.A[1] = ld16(w, offA + 1024u);
     x.GL = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(w, 0, (int)WS_GL, 0));
   };
-  auto fetch2 = [&](Rsrc w, Pre& x) {
+  auto fetch2 = [&](Rsrc w, Pre<NV>& x) {
     x.A[2] = ld16(w, offA + 2048u);
     x.A[3] = ld16(w, offA + 3072u);
-    if constexpr (URole) {
-      x.X = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w, offX, 0, 0));
-    } else {
-      const uint2 ob = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(w, offX, 0, 0));
-      x.X = make_uint4(ob.x, ob.y, 0, 0);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if constexpr (URole) {
+        x.X[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w, offX + v * XB, 0, 0));
+      } else {
+        const uint2 ob = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(w, offX + v * XB, 0, 0));
+        x.X[v] = make_uint4(ob.x, ob.y, 0, 0);
+      }
     }
   };
-  auto fetch3 = [&](Rsrc w, Pre& x) {
+  auto fetch3 = [&](Rsrc w, Pre<NV>& x) {
     x.KT[0] = ld16(w, offK);
     x.KT[1] = ld16(w, offK + 1024u);
   };
@@ -960,54 +970,67 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
     }
   };
 
-  auto process = [&](int ci, const Pre& cur, int ni, Pre& nxt) {
+  auto process = [&](int ci, const Pre<NV>& cur, int ni, Pre<NV>& nxt) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) sh.Ss[ss_w[i4]] = f32_to_bf16(S[i4]);
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) sh.Ss[v * VB * DK + ss_w[i4]] = f32_to_bf16(S[v][i4]);
     wait_ready(ni);
     const Rsrc wn = chunk_ws(ni);
     fetch1(wn, nxt);
     lds_barrier();
 
-    // [W'; Q'] S^T for this wave's 16 tokens, as two independent MFMA chains (half the dependent latency)
-    f32x4 x0 = zero4(), x1 = zero4();
+    float ov[NV][4];  // O role: this wave's outputs
 #pragma unroll
-    for (int kk = 0; kk < 4; kk += 2) {
-      x0 = mfma(cur.A[kk], ss_chunks[ss_r[kk]], x0);
-      x1 = mfma(cur.A[kk + 1], ss_chunks[ss_r[kk + 1]], x1);
-    }
-    const f32x4 x = x0 + x1;
-    float ov[4];  // O role: this wave's outputs
-    if constexpr (URole) {
-      // U' = Ub' - W' S^T as hi + lo bf16
-      const float ub[4] = {a.xs * __uint_as_float(cur.X.x), a.xs * __uint_as_float(cur.X.y),
-                           a.xs * __uint_as_float(cur.X.z), a.xs * __uint_as_float(cur.X.w)};
-      float u[4];
+    for (int v = 0; v < NV; ++v) {
+      // [W'; Q'] S^T for this wave's 16 tokens, as two independent MFMA chains (half the dependent latency)
+      f32x4 x0 = zero4(), x1 = zero4();
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) u[i4] = ub[i4] - x[i4];
-      const uint32_t h01 = pack_bf16x2(u[0], u[1]), h23 = pack_bf16x2(u[2], u[3]);
-      const uint32_t l01 = pack_bf16x2(u[0] - __uint_as_float(h01 << 16), u[1] - __uint_as_float(h01 & 0xffff0000u));
-      const uint32_t l23 = pack_bf16x2(u[2] - __uint_as_float(h23 << 16), u[3] - __uint_as_float(h23 & 0xffff0000u));
-      *reinterpret_cast<uint2*>(&sh.UhT[j][t0]) = make_uint2(h01, h23);
-      *reinterpret_cast<uint2*>(&sh.UlT[j][t0]) = make_uint2(l01, l23);
-    } else {
-      // O = Ob + Q' S^T (stored after the state update is issued)
-      const float ob[4] = {a.xs * __uint_as_float(cur.X.x << 16), a.xs * __uint_as_float(cur.X.x & 0xffff0000u),
-                           a.xs * __uint_as_float(cur.X.y << 16), a.xs * __uint_as_float(cur.X.y & 0xffff0000u)};
+      for (int kk = 0; kk < 4; kk += 2) {
+        x0 = mfma(cur.A[kk], ss_chunks[v * VB * DK / 8 + ss_r[kk]], x0);
+        x1 = mfma(cur.A[kk + 1], ss_chunks[v * VB * DK / 8 + ss_r[kk + 1]], x1);
+      }
+      const f32x4 x = x0 + x1;
+      const uint4 X = cur.X[v];
+      if constexpr (URole) {
+        // U' = Ub' - W' S^T as hi + lo bf16
+        const float ub[4] = {a.xs * __uint_as_float(X.x), a.xs * __uint_as_float(X.y), a.xs * __uint_as_float(X.z),
+                             a.xs * __uint_as_float(X.w)};
+        float u[4];
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) ov[i4] = ob[i4] + x[i4];
+        for (int i4 = 0; i4 < 4; ++i4) u[i4] = ub[i4] - x[i4];
+        const uint32_t h01 = pack_bf16x2(u[0], u[1]), h23 = pack_bf16x2(u[2], u[3]);
+        const uint32_t l01 = pack_bf16x2(u[0] - __uint_as_float(h01 << 16), u[1] - __uint_as_float(h01 & 0xffff0000u));
+        const uint32_t l23 = pack_bf16x2(u[2] - __uint_as_float(h23 << 16), u[3] - __uint_as_float(h23 & 0xffff0000u));
+        *reinterpret_cast<uint2*>(&sh.UhT[v * VB + j][t0]) = make_uint2(h01, h23);
+        *reinterpret_cast<uint2*>(&sh.UlT[v * VB + j][t0]) = make_uint2(l01, l23);
+      } else {
+        // O = Ob + Q' S^T (stored after the state update is issued)
+        const float ob[4] = {a.xs * __uint_as_float(X.x << 16), a.xs * __uint_as_float(X.x & 0xffff0000u),
+                             a.xs * __uint_as_float(X.y << 16), a.xs * __uint_as_float(X.y & 0xffff0000u)};
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) ov[v][i4] = ob[i4] + x[i4];
+      }
     }
     fetch2(wn, nxt);
     fetch3(wn, nxt);
     lds_barrier();
 
     // S <- exp(G_L) S + U'^T K for this wave's 16 columns (two chains over the key steps)
-    f32x4 acc0 = S * __expf(cur.GL), acc1 = zero4();
-    acc0 = mfma(frag(&sh.UhT[0][0], LDC, 0, 0), cur.KT[0], acc0);
-    acc1 = mfma(frag(&sh.UhT[0][0], LDC, 0, 32), cur.KT[1], acc1);
-    acc0 = mfma(frag(&sh.UlT[0][0], LDC, 0, 0), cur.KT[0], acc0);
-    acc1 = mfma(frag(&sh.UlT[0][0], LDC, 0, 32), cur.KT[1], acc1);
-    S = acc0 + acc1;
-    if constexpr (!URole) store_o_tile(o, a, ci, t0, j, ov);
+    const float decay = __expf(cur.GL);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      f32x4 acc0 = S[v] * decay, acc1 = zero4();
+      acc0 = mfma(frag(&sh.UhT[v * VB][0], LDC, 0, 0), cur.KT[0], acc0);
+      acc1 = mfma(frag(&sh.UhT[v * VB][0], LDC, 0, 32), cur.KT[1], acc1);
+      acc0 = mfma(frag(&sh.UlT[v * VB][0], LDC, 0, 0), cur.KT[0], acc0);
+      acc1 = mfma(frag(&sh.UlT[v * VB][0], LDC, 0, 32), cur.KT[1], acc1);
+      S[v] = acc0 + acc1;
+    }
+    if constexpr (!URole) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) store_o_tile(o, a, a.vb + v, ci, t0, j, ov[v]);
+    }
   };
 
   // two register buffers, alternately filled one chunk ahead (no copies between them). The fetches are
@@ -1016,7 +1039,7 @@ __device__ __forceinline__ void state_loop(StateShared& sh, const StateArgs& a, 
   // (which keeps the compiler's wait counts at the loop head from covering the prefetch). (Fetching two
   // chunks ahead, with a third buffer, measured no faster: the loop is bound by the per-CU load rate, not by
   // memory latency.)
-  Pre b0, b1;
+  Pre<NV> b0, b1;
   {
     if constexpr (Wait) fl = load_flag(fbase);
     wait_ready(0);
@@ -1059,20 +1082,21 @@ __device__ __forceinline__ size_t mt_frag(int n, int k) {
   return ((size_t)((w * 2 + t) * (DK / 32) + kb) * 64 + 16 * g + (n & 15)) * 8 + (k & 7);
 }
 
-template <typename TOut>
+template <typename TOut, int NV>
 __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
     const uint8_t* ws, const float* __restrict__ s_in, float* __restrict__ s_out, TOut* __restrict__ o,
     const int32_t* __restrict__ cu, int n_seqs, int n_chunks, int T, int Hv, const SegRun seg) {
   // (ws is not __restrict__: that keeps the compiler from sinking the prefetch loads below the LDS
   // barriers, whose asm memory clobber then pins them where they are issued)
-  __shared__ StateShared sh;
+  __shared__ StateSharedT<NV> sh;
+  constexpr int NG = DV / VB / NV;  // workgroups per (run, head): NV value blocks of 16 rows each
 
-  // XCD-aware order (workgroups go round-robin over the 8 XCDs): ids are taken in groups of 64 = 8 pairs
-  // (run, head) x 8 value blocks, with id % 8 = pair % 8, so the 8 workgroups of one pair run on one XCD at
-  // the same time and share its L2 copy of the chunk workspace. The grid is padded to whole groups.
+  // XCD-aware order (workgroups go round-robin over the 8 XCDs): ids are taken in groups of 8 NG = 8 pairs
+  // (run, head) x NG value-block groups, with id % 8 = pair % 8, so the NG workgroups of one pair run on one
+  // XCD at the same time and share its L2 copy of the chunk workspace. The grid is padded to whole groups.
   const int n_local = n_seqs * seg.G * Hv, n_trans = n_seqs * (seg.G - 1) * Hv;
   const int id = blockIdx.x;
-  const int pair = (id / 64) * 8 + (id % 8), vb = (id % 64) / 8;
+  const int pair = (id / (8 * NG)) * 8 + (id % 8), vb = ((id % (8 * NG)) / 8) * NV;  // first value block
   if (pair >= n_local + n_trans) return;
   const bool trans = pair >= n_local;
   const int vp = trans ? pair - n_local : pair;
@@ -1107,17 +1131,21 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   // chunks past the workspace (a chunk table shorter than the sequences need) are not read
   a.nchunks = max(0, min((a.len + CH - 1) / CH, n_chunks - a.c0));
 
-  // state slice in the D layout of the state update: rows j = 4*(l/16)+i, column ncol
-  f32x4 S;
-  const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;  // within one [V][K] state
+  // state slice in the D layout of the state update: block v, rows j = 4*(l/16)+i, column ncol
+  f32x4 S[NV];
   const size_t hs = (size_t)DV * DK;
-  if (trans) {
+  auto slice = [&](int v) { return ((size_t)(vb + v) * VB + 4 * (l >> 4)) * DK + ncol; };  // within a [V][K] state
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) S[i4] = vb * VB + 4 * (l >> 4) + i4 == ncol ? 1.f : 0.f;
-  } else {
+  for (int v = 0; v < NV; ++v) {
+    if (trans) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      S[i4] = s_in != nullptr && sg == 0 ? s_in[((size_t)seq * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
+      for (int i4 = 0; i4 < 4; ++i4) S[v][i4] = (vb + v) * VB + 4 * (l >> 4) + i4 == ncol ? 1.f : 0.f;
+    } else {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4)
+        S[v][i4] =
+            s_in != nullptr && sg == 0 ? s_in[((size_t)seq * Hv + h) * hs + slice(v) + (size_t)i4 * DK] : 0.f;
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // settle the state loads before the pipelined loop
 
@@ -1126,25 +1154,30 @@ __global__ __launch_bounds__(64 * P2_WAVES) void chunk_state_kernel(
   a.flag_step = 0;
   a.spin_max = 0;
   if (wave < 4)
-    state_loop<true, TOut, false>(sh, a, out, S);
+    state_loop<true, TOut, false, NV>(sh, a, out, S);
   else
-    state_loop<false, TOut, false>(sh, a, out, S);
+    state_loop<false, TOut, false, NV>(sh, a, out, S);
 
   if (trans) {  // the segment map transposed (M^T[n][k] = M[k][n]), as bf16 hi and lo parts [K][K] each
     uint16_t* mt = reinterpret_cast<uint16_t*>(seg.trans_final + ((size_t)run * Hv + h) * hs);
-    const size_t off = mt_frag(ncol, vb * VB + 4 * (l >> 4));
-    uint32_t h01, l01, h23, l23;
-    split2(S[0], S[1], h01, l01);
-    split2(S[2], S[3], h23, l23);
-    *reinterpret_cast<uint2*>(mt + off) = make_uint2(h01, h23);
-    *reinterpret_cast<uint2*>(mt + hs + off) = make_uint2(l01, l23);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const size_t off = mt_frag(ncol, (vb + v) * VB + 4 * (l >> 4));
+      uint32_t h01, l01, h23, l23;
+      split2(S[v][0], S[v][1], h01, l01);
+      split2(S[v][2], S[v][3], h23, l23);
+      *reinterpret_cast<uint2*>(mt + off) = make_uint2(h01, h23);
+      *reinterpret_cast<uint2*>(mt + hs + off) = make_uint2(l01, l23);
+    }
     return;
   }
   float* fin = seg.G > 1 ? seg.local_final + ((size_t)run * Hv + h) * hs
                          : s_out != nullptr ? s_out + ((size_t)seq * Hv + h) * hs : nullptr;
   if (fin != nullptr) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) fin[slice + (size_t)i4 * DK] = S[i4];
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) fin[slice(v) + (size_t)i4 * DK] = S[v][i4];
   }
 }
 
@@ -1335,18 +1368,18 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
       const int ncol = 16 * wave + (l & 15);
       const size_t slice = ((size_t)vb * VB + 4 * (l >> 4)) * DK + ncol;
       const size_t hs = (size_t)DV * DK;
-      f32x4 S;
+      f32x4 S[1];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4)
-        S[i4] = s_in != nullptr ? s_in[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
+        S[0][i4] = s_in != nullptr ? s_in[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] : 0.f;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       if (wave < 4)
-        state_loop<true, bf16, true>(sm.s, a, o, S);
+        state_loop<true, bf16, true, 1>(sm.s, a, o, S);
       else
-        state_loop<false, bf16, true>(sm.s, a, o, S);
+        state_loop<false, bf16, true, 1>(sm.s, a, o, S);
       if (s_out != nullptr) {
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) s_out[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] = S[i4];
+        for (int i4 = 0; i4 < 4; ++i4) s_out[((size_t)sq * Hv + h) * hs + slice + (size_t)i4 * DK] = S[0][i4];
       }
     }
     return;
@@ -1588,13 +1621,20 @@ __global__ __launch_bounds__(256) void chunk_correct_kernel(const uint16_t* __re
 // segmented one 80 a chunk of a segment, 207 a combine step and 985 fixed (the combine's and the correction's
 // launches and the longer state pass). A segment count in 2 .. 8 is taken when its local and transition
 // workgroups all fit one per CU and it is the cheapest.
+// NV: value blocks of 16 rows per state-pass workgroup. Two when the plain pass's workgroups of one block
+// would outnumber the CUs (more than n_cu / 8 chains): each then reads a chunk's shared operands (W' or Q',
+// K^T) once for 32 value rows, and the pass needs half the workgroup slots, for chunk steps about 1.4x as long
+// (measured: 32 packed sequences of 30,526 tokens at 16 heads, 4,096 one-block workgroups, 506 us with two
+// blocks against 552; one 4096-token sequence at 16 heads, 128 workgroups, 92.5 us with two against 73.6).
 struct SegPlan {
   int G, Cs;
+  int NV;
 };
+int state_nv(long chains, int n_cu) { return chains * (DV / VB) > n_cu ? 2 : 1; }
 SegPlan seg_plan(int B, int T, int Hv, int n_cu) {
   const int nct = (T + CH - 1) / CH;
   const long base = (long)B * Hv * (DV / VB);
-  SegPlan p{1, nct};
+  SegPlan p{1, nct, state_nv((long)B * Hv, n_cu)};
   if (nct < 8 || 2 * base > n_cu) return p;  // (a segment holds at least 4 chunks)
   long best = 64L * nct;
   for (int g = 2; g <= 8; ++g) {
@@ -1603,7 +1643,7 @@ SegPlan seg_plan(int B, int T, int Hv, int n_cu) {
     const long cost = 985 + 80L * cs + 207L * (gg - 1);
     if (cost < best) {
       best = cost;
-      p = SegPlan{gg, cs};
+      p = SegPlan{gg, cs, 1};
     }
   }
   return p;
@@ -1796,7 +1836,8 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
   uint8_t* ws = (uint8_t*)workspace;
   const bool gate = A_log != nullptr;
   // phase 2: plain runs, or (unpacked batches that would hold few CUs, workspace permitting) segmented runs
-  const SegPlan plan = cu_seqlens == nullptr ? seg_plan(B, T, Hv, device_cus()) : SegPlan{1, 0};
+  const SegPlan plan =
+      cu_seqlens == nullptr ? seg_plan(B, T, Hv, device_cus()) : SegPlan{1, 0, state_nv((long)N * Hv, device_cus())};
   const size_t base = zgdn_chunk_workspace_size(n_chunks, Hv);
   const bool segmented = plan.G > 1 && workspace_bytes >= base + seg_bytes(B, T, Hv, plan);
   SegRun run{1, (T + CH - 1) / CH, nullptr, nullptr, nullptr};
@@ -1855,9 +1896,14 @@ int chunk_fwd_impl(const char* fn, const void* q, const void* k, const void* v, 
                               N, T, scale, qk_l2norm, rs, ws, s);
   }
   const long runs = (long)N * Hv * (2 * run.G - 1);  // local + transition (run, head) pairs
-  dim3 grid2((unsigned)(((runs + 7) / 8) * 64));     // groups of 8 pairs x DV / VB = 8 value blocks
-  hipLaunchKernelGGL((chunk_state_kernel<bf16>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state, final_state,
-                     (bf16*)o, cu_seqlens, N, n_chunks, T, Hv, run);
+  // groups of 8 pairs x DV / VB / NV value-block groups
+  const dim3 grid2((unsigned)(((runs + 7) / 8) * 8 * (DV / VB / plan.NV)));
+  if (plan.NV == 2)
+    hipLaunchKernelGGL((chunk_state_kernel<bf16, 2>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state,
+                       final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hv, run);
+  else
+    hipLaunchKernelGGL((chunk_state_kernel<bf16, 1>), grid2, dim3(64 * P2_WAVES), 0, s, ws, initial_state,
+                       final_state, (bf16*)o, cu_seqlens, N, n_chunks, T, Hv, run);
   if (segmented) {
     hipLaunchKernelGGL(chunk_combine_kernel, dim3(N * Hv * (DV / CB_ROWS)), dim3(256), 0, s, run.local_final,
                        run.trans_final, s_start, final_state, Hv, run.G);
