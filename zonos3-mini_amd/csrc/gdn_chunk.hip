@@ -342,8 +342,9 @@ struct ItemWalk {
   }
 };
 
-// The chunk's rows of q, k, v for thread (rr, c8): rows rr and rr + 32, columns c8 .. c8 + 7 (zeros past the
-// chunk end).
+// The chunk's rows of q, k, v for thread (rr, c8): rows rr and rr + 32 (W = 8 waves) or row rr (W = 16),
+// columns c8 .. c8 + 7 (zeros past the chunk end).
+template <int W>
 __device__ __forceinline__ void load_rows(RowRegs& R, const ItemAt& it, const uint16_t* q, const uint16_t* k,
                                           const uint16_t* v, const RowStrides& rs, uint32_t oq, uint32_t ok,
                                           uint32_t ov) {
@@ -354,15 +355,17 @@ __device__ __forceinline__ void load_rows(RowRegs& R, const ItemAt& it, const ui
   R.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq, 0, 0));
   R.k0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok, 0, 0));
   R.v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, ov, 0, 0));
-  R.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq + 64u * (uint32_t)rs.q, 0, 0));
-  R.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 64u * (uint32_t)rs.k, 0, 0));
-  R.v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, ov + 64u * (uint32_t)rs.v, 0, 0));
+  if constexpr (W == 8) {
+    R.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq + 64u * (uint32_t)rs.q, 0, 0));
+    R.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 64u * (uint32_t)rs.k, 0, 0));
+    R.v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, ov + 64u * (uint32_t)rs.v, 0, 0));
+  }
 }
 
 // Once per workgroup: the blocks of P^T that stay zero (P's blocks above its diagonal blocks).
 __device__ __forceinline__ void prep_init(uint8_t* lb) {
   // P^T physical blocks (pr, pc) with pr > pc: (1,0), (2,0), (2,1), (3,0), (3,1), (3,2); 512 bytes each
-  for (int e = threadIdx.x; e < 6 * 32; e += P1_THREADS) {
+  for (int e = threadIdx.x; e < 6 * 32; e += blockDim.x) {
     const int t = e >> 5, w = e & 31;
     const int pr = t < 1 ? 1 : (t < 3 ? 2 : 3), pc = t - pr * (pr - 1) / 2;
     const int row = 16 * pr + (w >> 1), c8 = 16 * pc + 8 * (w & 1);  // 8 bf16 of a row
@@ -378,8 +381,10 @@ __device__ __forceinline__ void item_barrier() { asm volatile("s_waitcnt lgkmcnt
 // One phase-1 item (`it`). `R` holds the item's rows (loaded by the caller); with `has_next`, the rows of item
 // `nx` are loaded into R while this one computes. QL: the raw q of the Q' step is taken from the q rows in LDS
 // (held in registers from step 2 on; no second read of q from memory), else read again from memory before step
-// 6 (fewer registers held: the overlapped kernel's budget). Ends with a workgroup barrier.
-template <typename TG, bool GATE, bool QL>
+// 6 (fewer registers held: the overlapped kernel's budget). W: the workgroup's waves, 8 (two workgroups a CU) or
+// 16 (one item a CU when the items are few: the phases spread over twice the waves, the item's latency
+// shorter). Ends with a workgroup barrier.
+template <typename TG, bool GATE, bool QL, int W>
 __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs& R, bool has_next, const ItemAt& nx,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
@@ -401,10 +406,14 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   const ChunkRange cr = it.cr;
   uint8_t* wsc = ws + ((size_t)c * Hv + h) * WS_CHUNK;
   float* F = reinterpret_cast<float*>(lb + PS_F);
+  static_assert(W == 8 || W == 16, "8 or 16 waves an item");
+  constexpr int NJ16 = 16 / W;                 // a wave's jobs of 16
+  constexpr int NJ = (16 + W - 2) / (W - 1);   // a wave's jobs of the 16 off-diagonal K K^T / Q K^T tiles
+  constexpr int TBN = 4 * 8 / W;               // token tiles of a wave's value block (steps 7, 8)
 
   // gate inputs (wave 7), issued before the row stores
   float gi = 0.f, bi = 0.f, alog = 0.f, dtb = 0.f;
-  if (wave == P1_WAVES - 1 && l < cr.len) {
+  if (wave == W - 1 && l < cr.len) {
     const size_t gh = (size_t)(cr.t0 + l) * rs.gb + h;
     gi = io<TG>::load(g + gh);
     bi = io<TG>::load(beta + gh);
@@ -415,13 +424,15 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   }
   // 1. rows -> LDS; the next item's rows into the registers
   lds_put<uint4>(lb, PS_Q + rowoff, R.q0);
-  lds_put<uint4>(lb, PS_Q + rowoff + 8192, R.q1);
   lds_put<uint4>(lb, PS_K + rowoff, R.k0);
-  lds_put<uint4>(lb, PS_K + rowoff + 8192, R.k1);
   lds_put<uint4>(lb, PS_V + rowoff, R.v0);
-  lds_put<uint4>(lb, PS_V + rowoff + 8192, R.v1);
-  if (has_next) load_rows(R, nx, q, k, v, rs, oq, ok, ov);
-  if (wave == P1_WAVES - 1) {
+  if constexpr (W == 8) {
+    lds_put<uint4>(lb, PS_Q + rowoff + 8192, R.q1);
+    lds_put<uint4>(lb, PS_K + rowoff + 8192, R.k1);
+    lds_put<uint4>(lb, PS_V + rowoff + 8192, R.v1);
+  }
+  if (has_next) load_rows<W>(R, nx, q, k, v, rs, oq, ok, ov);
+  if (wave == W - 1) {
     if (l < cr.len) {
       if constexpr (GATE) gi = -__expf(alog) * softplus(gi + dtb);
       if (rs.beta_sigmoid) bi = sigmoid(bi);
@@ -472,11 +483,11 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   }
   // raw q of this wave's Q' jobs (step 8): token 16 tb + m, columns 32 kq + 4 gq .. + 3 and 16 further; with QL
   // from the q rows, before A^T overwrites them (rows past the chunk end hold zeros)
-  uint2 cq[2][2];
+  uint2 cq[NJ16][2];
   if constexpr (QL) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
+    for (int n = 0; n < NJ16; ++n) {
+      const int job = wave + W * n, tb = job >> 2, kq = job & 3;
       const int tok = 16 * tb + m, cc = 4 * kq + (gq >> 1);
       const int at = PS_Q + tok * 256 + 8 * (gq & 1);
       cq[n][0] = lds_at<uint2>(lb, at + ((cc ^ m) << 4));
@@ -484,8 +495,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
     }
   }
   f32x4 acc[4];
-  int jrb[3], jcb[3];
-  bool jqk[3];
+  int jrb[NJ], jcb[NJ];
+  bool jqk[NJ];
   if (wave == 0) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -498,8 +509,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
     }
   } else {
 #pragma unroll
-    for (int n = 0; n < 3; ++n) {
-      const int j = wave - 1 + 7 * n;
+    for (int n = 0; n < NJ; ++n) {
+      const int j = wave - 1 + (W - 1) * n;
       jrb[n] = jcb[n] = 0;
       jqk[n] = false;
       acc[n] = zero4();
@@ -573,8 +584,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
       lds_put<f32x4>(lb, roww ^ (qd << 4), f32x4{sv[4 * qd], sv[4 * qd + 1], sv[4 * qd + 2], sv[4 * qd + 3]});
   } else {
 #pragma unroll
-    for (int n = 0; n < 3; ++n) {
-      if (wave - 1 + 7 * n < 16) {
+    for (int n = 0; n < NJ; ++n) {
+      if (wave - 1 + (W - 1) * n < 16) {
         const f32x4 e = scale_tile(acc[n], jrb[n], jcb[n], jqk[n]);
         if (jqk[n]) put_t16(lb, PS_PT, jrb[n], jcb[n], L, e);
         else put_t32(lb, PS_AT, jrb[n], jcb[n], L, e);
@@ -612,7 +623,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   // TBF^T[j][i] = Fk_i T_ij... = Fk_i T[i][j] Bk_j, TBT[j][i] = T[i][j] Bk_j, LB^T[j][i] = (T - I)[i][j] beta_j;
   // T's blocks above its diagonal blocks (pair products there) are zero
   {
-    const int j = tid >> 3, i0 = (tid & 7) * 8;
+    const bool act = W == 8 || tid < 512;  // (512 threads: 8 a row of T^T)
+    const int j = (tid >> 3) & 63, i0 = (tid & 7) * 8;
     const int rd = PS_TT + j * 256 + (((2 * (tid & 7)) ^ (j & 15)) << 4);
     f32x4 t0 = lds_at<f32x4>(lb, rd), t1 = lds_at<f32x4>(lb, rd ^ 16);
     if ((i0 >> 4) < (j >> 4)) t0 = t1 = zero4();
@@ -630,16 +642,18 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
     }
     item_barrier();  // the forms overwrite T^T and A^T
     const int wr = j * 128 + ((((tid & 7) ^ ((j >> 1) & 7))) << 4);
-    lds_put<uint4>(lb, PS_TBF + wr, make_uint4(wf[0], wf[1], wf[2], wf[3]));
-    lds_put<uint4>(lb, PS_TBT + wr, make_uint4(wt[0], wt[1], wt[2], wt[3]));
-    lds_put<uint4>(lb, PS_LB + wr, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+    if (act) {
+      lds_put<uint4>(lb, PS_TBF + wr, make_uint4(wf[0], wf[1], wf[2], wf[3]));
+      lds_put<uint4>(lb, PS_TBT + wr, make_uint4(wt[0], wt[1], wt[2], wt[3]));
+      lds_put<uint4>(lb, PS_LB + wr, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+    }
   }
   item_barrier();
 
   if constexpr (!QL) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3;
+    for (int n = 0; n < NJ16; ++n) {
+      const int job = wave + W * n, tb = job >> 2, kq = job & 3;
       const int tok = 16 * tb + m;
       cq[n][0] = cq[n][1] = make_uint2(0, 0);
       if (tok < cr.len) {
@@ -655,8 +669,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   {
     uint4* gW = reinterpret_cast<uint4*>(wsc + WS_WP);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
+    for (int n = 0; n < NJ16; ++n) {
+      const int job = wave + W * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
       f32x4 d0 = zero4(), d1 = zero4();
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
@@ -668,8 +682,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
       gW[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
     }
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {  // R tiles: jobs 0-9 the lower tiles, 10-15 zero tiles above
-      const int job = wave + P1_WAVES * n;
+    for (int n = 0; n < NJ16; ++n) {  // R tiles: jobs 0-9 the lower tiles, 10-15 zero tiles above
+      const int job = wave + W * n;
       int rb, cb;
       if (job < 10) {
         lower_tile(job, rb, cb);
@@ -687,8 +701,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
     }
     uint4* gKT = reinterpret_cast<uint4*>(wsc + WS_KT);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {  // fragment f = 2 w + kk = wave + 8 n (16 fragments of 64 lanes)
-      const int f = wave + P1_WAVES * n;
+    for (int n = 0; n < NJ16; ++n) {  // fragment f = 2 w + kk = wave + W n (16 fragments of 64 lanes)
+      const int f = wave + W * n;
       gKT[f * 64 + l] = __builtin_bit_cast(uint4, pfragT16(lb, PS_K, 16 * (f >> 1), f & 1, L));
     }
   }
@@ -697,9 +711,10 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   // 7. Ub = beta V + LB V: Ub' = Fk Ub (fp32 D tiles) to the workspace, Ub^T (bf16) to LDS
   {
     float4* gU = reinterpret_cast<float4*>(wsc + WS_UB);
-    const int vb = wave;
+    const int vb = wave & 7;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tt = 0; tt < TBN; ++tt) {
+      const int tb = (wave >> 3) * TBN + tt;
       f32x4 u = zero4();
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
@@ -723,8 +738,8 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
   {
     uint4* gQ = reinterpret_cast<uint4*>(wsc + WS_QP);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int job = wave + P1_WAVES * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
+    for (int n = 0; n < NJ16; ++n) {
+      const int job = wave + W * n, tb = job >> 2, kq = job & 3, nk = tri_kend(tb) / 32;
       f32x4 d0 = zero4(), d1 = zero4();
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
@@ -746,9 +761,10 @@ __device__ __forceinline__ void prep_item(uint8_t* lb, const ItemAt& it, RowRegs
       gQ[(tb * 4 + kq) * 64 + l] = kappa_frag(d0, d1);
     }
     uint2* gO = reinterpret_cast<uint2*>(wsc + WS_OB);
-    const int vb = wave;
+    const int vb = wave & 7;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tt = 0; tt < TBN; ++tt) {
+      const int tb = (wave >> 3) * TBN + tt;
       f32x4 y = zero4();
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
@@ -774,8 +790,9 @@ struct PrepRows {
   }
 };
 
-template <typename TG, bool GATE>
-__global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
+// W = 8: two workgroups a CU; W = 16: one (the same registers a wave).
+template <typename TG, bool GATE, int W>
+__global__ __launch_bounds__(64 * W, P1_WAVES_PER_SIMD) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const TG* __restrict__ g, const TG* __restrict__ beta, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const int32_t* __restrict__ cu, const int32_t* __restrict__ chunk_idx,
@@ -790,13 +807,13 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_prep_kern
   ItemWalk w(blockIdx.x, gridDim.x, Hv, Hk, T);
   if (w.item >= n_items) return;
   ItemAt cur = w.at(cu, chunk_idx, n_seqs, T);  // (a packed batch's chunk table is read for items < n_items only)
-  load_rows(R, cur, q, k, v, rs, lr.oq, lr.ok, lr.ov);
+  load_rows<W>(R, cur, q, k, v, rs, lr.oq, lr.ok, lr.ov);
   while (w.item < n_items) {
     w.advance();
     const bool has_next = w.item < n_items;
     ItemAt nx = cur;
     if (has_next) nx = w.at(cu, chunk_idx, n_seqs, T);
-    prep_item<TG, GATE, true>(lb, cur, R, has_next, nx, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs, ws, L,
+    prep_item<TG, GATE, true, W>(lb, cur, R, has_next, nx, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs, ws, L,
                         lr.rowoff, lr.oq, lr.ok, lr.ov);
     cur = nx;
   }
@@ -1421,7 +1438,7 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
   int cur = tk;
   __syncthreads();  // every thread has read tk
   if (cur >= 0 && cur < n_items)
-    load_rows(R, item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
+    load_rows<P1_WAVES>(R, item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
   while (cur >= 0) {
     if (threadIdx.x == 0) tk = take();
     __syncthreads();  // tk visible (and the LDS of the last item is free)
@@ -1430,13 +1447,14 @@ __global__ __launch_bounds__(P1_THREADS, P1_WAVES_PER_SIMD) void chunk_fused_ker
     if (cur < n_items) {
       const ItemAt ic = item_at(cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
       const ItemAt in = item_at(nload >= 0 ? nload : cur, cu, chunk_idx, n_seqs, T, Hk, Hv);
-      prep_item<TG, GATE, false>(sm.p.b, ic, R, nload >= 0, in, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs,
+      prep_item<TG, GATE, false, P1_WAVES>(sm.p.b, ic, R, nload >= 0, in, q, k, v, g, beta, A_log, dt_bias, Hv, scale, qk_l2norm, rs,
                           ws, L, lr.rowoff, lr.oq, lr.ok, lr.ov);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's workspace stores are in the L2
       __syncthreads();
       if (threadIdx.x == 0) __hip_atomic_store(ctl.flags + cur, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
-      if (nload >= 0) load_rows(R, item_at(nload, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
+      if (nload >= 0)
+        load_rows<P1_WAVES>(R, item_at(nload, cu, chunk_idx, n_seqs, T, Hk, Hv), q, k, v, rs, lr.oq, lr.ok, lr.ov);
       __syncthreads();  // every thread has read tk
     }
     cur = nxt;
@@ -1718,15 +1736,21 @@ void launch_prep(bool gate, int nchunks, int Hk, int Hv, const void* q, const vo
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     n_cu = 256;
   const int n_items = nchunks * Hv;
-  dim3 grid(std::min(n_items, P1_WGS_PER_CU * std::max(1, n_cu)));
-  if (gate)
-    hipLaunchKernelGGL((chunk_prep_kernel<TG, true>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, rs, ws);
-  else
-    hipLaunchKernelGGL((chunk_prep_kernel<TG, false>), grid, dim3(P1_THREADS), 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,
-                       chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, rs, ws);
+  // at most one item a CU: one workgroup of 16 waves each (the item's latency is the phase's time)
+  const bool wide = n_items <= std::max(1, n_cu);
+  const dim3 grid(wide ? n_items : std::min(n_items, P1_WGS_PER_CU * std::max(1, n_cu)));
+#define ZGDN_PREP(GT, WV)                                                                                          \
+  hipLaunchKernelGGL((chunk_prep_kernel<TG, GT, WV>), grid, dim3(64 * (WV)), 0, stream, (const uint16_t*)q,       \
+                     (const uint16_t*)k, (const uint16_t*)v, (const TG*)g, (const TG*)beta, A_log, dt_bias, cu,    \
+                     chunk_idx, n_seqs, n_items, T, Hk, Hv, scale, qk_l2norm, rs, ws)
+  if (gate) {
+    if (wide) ZGDN_PREP(true, 16);
+    else ZGDN_PREP(true, 8);
+  } else {
+    if (wide) ZGDN_PREP(false, 16);
+    else ZGDN_PREP(false, 8);
+  }
+#undef ZGDN_PREP
 }
 
 }  // namespace
