@@ -134,3 +134,24 @@ def test_rows_read_in_place(gdn, cuda):
     g2, _ = gdn.ops.gated_rmsnorm(o, rows.contiguous(), nw, eps=1e-5)
     torch.cuda.synchronize()
     assert torch.equal(g1, g2)
+
+
+def test_gated_norm_many_rows(gdn, cuda):
+    """Many rows (4101 tokens x 4 heads, 1026 workgroups with a ragged last one), the gate read in place from
+    wider rows: within the bf16 tolerance of the oracle, rstd the row's 1/rms, and every row bit-identical to
+    the same row normed in a small call."""
+    announce("gated rmsnorm, many rows")
+    gen = torch.Generator().manual_seed(3211)
+    T = 4101
+    o = torch.randn(T, 4, 128, generator=gen).to(torch.bfloat16).to(cuda)
+    buf = torch.randn(T, 4 * 128 + 24, generator=gen).to(torch.bfloat16).to(cuda)
+    z = buf[:, :512].unflatten(-1, (4, 128))
+    nw = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16).to(cuda)
+    got, rstd = gdn.ops.gated_rmsnorm(o, z, nw, eps=1e-5)
+    want = O.gated_rmsnorm(o.cpu(), z.cpu(), nw.cpu(), 1e-5, torch.bfloat16)
+    assert max_abs(got.cpu(), want) < 2e-2
+    assert rel_err(rstd.cpu(), torch.rsqrt(o.float().square().mean(-1) + 1e-5).cpu()) < 1e-5
+    for sl in (slice(0, 20), slice(2000, 2013), slice(T - 21, T)):
+        g2, r2 = gdn.ops.gated_rmsnorm(o[sl], z[sl], nw, eps=1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(got[sl], g2) and torch.equal(rstd[sl], r2), sl
