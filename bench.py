@@ -90,6 +90,27 @@ def kernel_ms(torch, stream, fn, n):
     return start.elapsed_time(end) / n
 
 
+def steady_ms(torch, stream, fn, n, warm=50):
+    """Mean duration (ms) of one call of ``fn`` at steady state: ``n`` calls timed with HIP events on the
+    launch stream behind ``warm`` untimed calls queued ahead, so that the GPU runs them back to back at the
+    clocks a busy GPU holds. For calls whose GPU time exceeds their host time (the host then stays ahead of
+    the queue; were it not, the GPU would wait and the figure could only grow). kernel_ms's sleep leaves the
+    GPU idle for milliseconds first, and the calls right after it run a few percent slower."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        for _ in range(warm):
+            fn()
+        start.record(stream)
+        for _ in range(n):
+            fn()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n
+
+
 def bench_decode(torch, gdn, steps, warmup):
     dev = torch.device("cuda:0")
     _, x, state = _decode_inputs(torch, dev)
@@ -136,7 +157,7 @@ _C, _K, _V = PREFILL["C"], PREFILL["K"], PREFILL["V"]
 PREFILL_FLOP_PER_CHUNK_HEAD = 2 * _C * _C * (3 * _K + 2 * _V) + 6 * _C * _K * _V + _C**3 / 3
 
 
-def bench_prefill(torch, gdn, reps=50):
+def bench_prefill(torch, gdn, reps=200):
     from oracle import gdn_oracle as O
 
     dev = torch.device("cuda:0")
@@ -148,10 +169,10 @@ def bench_prefill(torch, gdn, reps=50):
     def run():
         return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
 
-    ms = kernel_ms(torch, stream, run, reps)
+    ms = steady_ms(torch, stream, run, reps)
     # the same call through the overlapped launch (phase 1 and the state pass side by side), for comparison
     with gdn.ops.launch_form(1):
-        ms_overlapped = kernel_ms(torch, stream, run, reps)
+        ms_overlapped = steady_ms(torch, stream, run, reps)
     flops = PREFILL_FLOP_PER_CHUNK_HEAD * (c["T"] // c["C"]) * c["H"] * c["B"]
     tflops = flops / (ms * 1e-3) / 1e12
     return {
@@ -171,7 +192,7 @@ def bench_prefill(torch, gdn, reps=50):
     }
 
 
-def bench_prefill_f32(torch, gdn, reps=20):
+def bench_prefill_f32(torch, gdn, reps=50):
     """The chunked prefill in fp32 (the layer's fp32 dtype, lm.py:556-602): the prefill workload's shape with
     fp32 q/k/v/o (T=4096, H=16, d=128), and the CPU-oracle configuration (B=1, T=256, H=4, d=64, fp32) with
     its CPU time beside it. fp32 arithmetic throughout, so the roofline is the fp32 matrix peak."""
@@ -188,7 +209,8 @@ def bench_prefill_f32(torch, gdn, reps=20):
         def run():
             return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"])
 
-        ms = kernel_ms(torch, stream, run, reps)
+        # (the 256-token case is host-bound at steady state: timed behind kernel_ms's sleep)
+        ms = steady_ms(torch, stream, run, reps) if T >= 4096 else kernel_ms(torch, stream, run, reps)
         flops = (2 * _C * _C * 5 * D + 6 * _C * D * D + _C**3 / 3) * (-(-T // _C)) * H * B
         tflops = flops / (ms * 1e-3) / 1e12
         out[name] = {
@@ -219,7 +241,7 @@ def varlen_lengths(torch):
     return torch.randint(VARLEN["lo"], VARLEN["hi"] + 1, (VARLEN["n_seqs"],), generator=g).tolist()
 
 
-def bench_varlen(torch, gdn, reps=20):
+def bench_varlen(torch, gdn, reps=50):
     """Packed prefill: 32 sequences of seeded lengths in [64, 2048], one token stream with cu_seqlens,
     per-sequence initial states ~N(0, 0.02)."""
     from oracle import gdn_oracle as O
@@ -238,9 +260,9 @@ def bench_varlen(torch, gdn, reps=20):
         return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t,
                              chunk_indices=ch_t)
 
-    ms = kernel_ms(torch, stream, run, reps)
+    ms = steady_ms(torch, stream, run, reps, warm=20)
     with gdn.ops.launch_form(1):
-        ms_overlapped = kernel_ms(torch, stream, run, reps)
+        ms_overlapped = steady_ms(torch, stream, run, reps, warm=20)
     flops = PREFILL_FLOP_PER_CHUNK_HEAD / PREFILL["C"] * total * c["H"]
     tflops = flops / (ms * 1e-3) / 1e12
     return {
