@@ -90,18 +90,27 @@ def kernel_ms(torch, stream, fn, n):
     return start.elapsed_time(end) / n
 
 
-def steady_ms(torch, stream, fn, n, warm=50):
+STEADY_WARM_S = 0.02  # untimed work queued ahead of steady-state timings (seconds of calls)
+
+
+def steady_ms(torch, stream, fn, n):
     """Mean duration (ms) of one call of ``fn`` at steady state: ``n`` calls timed with HIP events on the
-    launch stream behind ``warm`` untimed calls queued ahead, so that the GPU runs them back to back at the
-    clocks a busy GPU holds. For calls whose GPU time exceeds their host time (the host then stays ahead of
-    the queue; were it not, the GPU would wait and the figure could only grow). kernel_ms's sleep leaves the
-    GPU idle for milliseconds first, and the calls right after it run a few percent slower."""
+    launch stream behind about 20 ms of untimed calls queued ahead, so that the GPU runs them back to back at
+    the clocks a busy GPU holds (measured at T = 4096, 16 heads: the prefill reads 71.3-72.0 us behind 3.6 ms of
+    calls, 68.8-69.2 us behind 14-42 ms). For calls whose GPU time exceeds their host time (the host then stays
+    ahead of the queue; were it not, the GPU would wait and the figure could only grow). kernel_ms's sleep
+    leaves the GPU idle for milliseconds first, and the calls right after it run a few percent slower."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         fn()
         torch.cuda.synchronize()
-        for _ in range(warm):
+        t0 = time.perf_counter()
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        per_call = (time.perf_counter() - t0) / 5
+        for _ in range(max(10, int(STEADY_WARM_S / per_call) + 1)):
             fn()
         start.record(stream)
         for _ in range(n):
@@ -260,9 +269,9 @@ def bench_varlen(torch, gdn, reps=50):
         return gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t,
                              chunk_indices=ch_t)
 
-    ms = steady_ms(torch, stream, run, reps, warm=20)
+    ms = steady_ms(torch, stream, run, reps)
     with gdn.ops.launch_form(1):
-        ms_overlapped = steady_ms(torch, stream, run, reps, warm=20)
+        ms_overlapped = steady_ms(torch, stream, run, reps)
     flops = PREFILL_FLOP_PER_CHUNK_HEAD / PREFILL["C"] * total * c["H"]
     tflops = flops / (ms * 1e-3) / 1e12
     return {
@@ -386,7 +395,6 @@ def bench_attnres(torch, gdn):
 
 SERVING = dict(hidden=1024, prompt=100, batch_sizes=(2, 32))
 LAYER_T = (4096, 1024)  # prompt lengths of the layer-level prefill line
-LAYER_WARM_REPLAYS = 50  # untimed graph replays queued ahead of the timed ones
 ACCENT = dict(rows=4096, **{"in": 1024}, out=2056, K=64)
 
 
@@ -517,16 +525,7 @@ def bench_layer_prefill(torch, reps=200):
             # steady state: the timed replays queued behind untimed ones, so that the GPU never waits for the
             # host between them and runs at the clocks a busy server sees (GPU time per call); the eager calls
             # on their own (their host time is the point)
-            torch.cuda.synchronize()
-            for _ in range(LAYER_WARM_REPLAYS):
-                graph.replay()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            for _ in range(reps):
-                graph.replay()
-            end.record(stream)
-            torch.cuda.synchronize()
-            timings["graph"] = start.elapsed_time(end) / reps * 1e3
+            timings["graph"] = steady_ms(torch, stream, graph.replay, reps) * 1e3
             call()
             torch.cuda.synchronize()
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
