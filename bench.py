@@ -109,7 +109,7 @@ def steady_ms(torch, stream, fn, n):
         for _ in range(5):
             fn()
         torch.cuda.synchronize()
-        per_call = (time.perf_counter() - t0) / 5
+        per_call = max((time.perf_counter() - t0) / 5, 1e-5)
         for _ in range(max(10, int(STEADY_WARM_S / per_call) + 1)):
             fn()
         start.record(stream)
