@@ -63,6 +63,22 @@ def test_prefill_T16384_H16(gdn, cuda):
     _check(o.cpu(), s.cpu(), o_ref, s_ref)
 
 
+def test_prefill_T65536_H4_segmented(gdn, cuda):
+    """A 65,536-token prompt at the release model's 4 heads (initial states ~N(0, 0.02)): the segmented state
+    pass at its longest segments (4 segments of 256 chunks, three combine steps). Against the token-loop
+    recurrent kernel (fp32 state; itself checked against the oracle) within the oracle tolerance: the state
+    error does not grow with the segment length."""
+    announce("chunk prefill T=65536 H=4 (segmented)")
+    assert int(gdn._native.lib().zgdn_chunk_segment_workspace_size(1, 65536, 4)) > 0  # the path is taken
+    d = O.make_inputs(1, 65536, 4, 4, 128, 128, seed=1065, dtype=torch.bfloat16, state_std=0.02)
+    x = _dev(d, cuda)
+    o, s = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"])
+    o_ref, s_ref = gdn.recurrent_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"],
+                                     out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(o.cpu(), s.cpu(), o_ref.cpu(), s_ref.cpu())
+
+
 def test_packed_sequences(gdn, cuda):
     lengths = [64, 1, 130, 0, 70, 200, 63]
     cu, _ = O.chunk_tables(lengths)
