@@ -94,6 +94,29 @@ def test_packed_sequences(gdn, cuda):
     assert torch.equal(s[3].cpu(), d["s0"][3])  # the empty sequence keeps its state
 
 
+def test_many_short_packed_sequences(gdn, cuda):
+    """300 packed sequences, most of 0-3 tokens and some at the chunk edges, with one of 2,000 tokens in the
+    middle, grouped heads (2 key, 4 value): more sequences than the overlapped launch takes and 1,200 chains
+    (two value blocks per state workgroup). Against the oracle; empty sequences keep their states."""
+    gen = torch.Generator().manual_seed(2131)
+    pool = [0, 1, 2, 3, 1, 2, 63, 64, 65]
+    lengths = [pool[int(i)] for i in torch.randint(0, len(pool), (300,), generator=gen)]
+    lengths[150] = 2000
+    cu, _ = O.chunk_tables(lengths)
+    announce(f"chunk varlen {len(lengths)} sequences, {sum(lengths)} tokens")
+    d = O.make_inputs(1, sum(lengths), 2, 4, 128, 128, seed=2132, dtype=torch.bfloat16, state_std=0.02,
+                      n_states=len(lengths))
+    x = _dev(d, cuda)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=cuda)
+    o, s = gdn.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["s0"], cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    o_ref, s_ref = O.gated_delta_recurrence(d["q"], d["k"], d["v"], d["g"], d["beta"], None, d["s0"], cu_seqlens=cu)
+    _check(o.cpu(), s.cpu(), o_ref, s_ref)
+    for i, n in enumerate(lengths):
+        if n == 0:
+            assert torch.equal(s[i].cpu(), d["s0"][i])
+
+
 def test_grouped_heads_gate_in_kernel_and_bf16_gates(gdn, cuda):
     """Hk=8 -> Hv=16; the decay formed in the kernel from raw a, A_log, dt_bias; bf16 a and beta."""
     announce("chunk GVA 8->16, in-kernel gate, bf16 gates")
